@@ -1,0 +1,946 @@
+// HBM-resident FragPack KV store on gfx950: per-step bookkeeping, the
+// kernel-order staging writer, the record encoder, the decode-to-workspace
+// gather, block-blob export/import and the batch record codec.
+//
+// Reference: fragpack/ops/hbm_kv.cu (prepare :110-219, write :221-255,
+// encode :257-429, commit :431-448, gather :450-494, blobs :496-665) and the
+// state machine in fragpack/ops/hbm_kv.py:1-47.  The bookkeeping kernels keep
+// the reference's state layout and counter semantics, since the Python host
+// side and the tests read them; the encoder produces the reference codec's
+// exact bytes (fragpack/compression/attn_page.py:146-209).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fragpack_hip.h"
+#include "fp_capi_internal.hpp"
+#include "fp_record.hpp"
+
+namespace fp {
+namespace {
+
+// Counter slots (int32[16]), the reference's numbering (hbm_kv.cu:14-26).
+enum : int {
+  kFreeTop = 0,
+  kTrans = 1,
+  kClaims = 2,
+  kCloses = 3,
+  kErrStaging = 4,
+  kErrOverflow = 5,
+  kFallbacks = 6,
+  kEncoded = 7,
+  kSpills = 8,
+  kHeirs = 9,
+  kDonors = 10,
+};
+enum : int { kTagLive = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
+
+constexpr int kPrepThreads = 1024;
+constexpr int kThreads = 256;
+
+struct Store {
+  int32_t* counters;
+  int32_t* wslot;
+  int32_t* tags;
+  int32_t* free_stack;
+  uint32_t* ovf_bits;
+  int32_t* claim_list;
+  int32_t* close_list;
+  int64_t* rec_addr;
+  int32_t* rec_len;
+  uint8_t* staging;
+  uint8_t* scratch;
+  uint8_t* ovf_base;
+  int32_t* fill;
+  int64_t ovf_bytes;
+  int L, H, NB, S_p, S_t, ovf_words, cap;
+};
+
+Store make_store(const fp_store_t* d) {
+  Store s;
+  s.counters = d->counters;
+  s.wslot = d->wslot;
+  s.tags = d->tags;
+  s.free_stack = d->free_stack;
+  s.ovf_bits = d->ovf_bits;
+  s.claim_list = d->claim_list;
+  s.close_list = d->close_list;
+  s.rec_addr = d->rec_addr;
+  s.rec_len = d->rec_len;
+  s.staging = d->staging;
+  s.scratch = d->scratch;
+  s.ovf_base = d->overflow;
+  s.fill = d->fill;
+  s.ovf_bytes = d->overflow_records * (int64_t)kRawRecord;
+  s.L = (int)d->num_layers;
+  s.H = (int)d->kv_heads;
+  s.NB = (int)d->num_blocks;
+  s.S_p = (int)d->staging_slots;
+  s.S_t = (int)d->scratch_slots;
+  s.ovf_words = (int)d->ovf_words;
+  s.cap = (int)d->list_cap;
+  return s;
+}
+
+int check_store(const fp_store_t* d) {
+  FP_CHECK(d != nullptr, "store descriptor is null");
+  FP_CHECK(d->num_layers > 0 && d->num_blocks > 0 && d->kv_heads > 0, "store geometry must be positive");
+  FP_CHECK(d->num_blocks < (1 << 30) && d->list_cap >= 0 && d->list_cap < (1 << 30), "store too large");
+  return 0;
+}
+
+// Record (kv * H + h) of the block staged in slot ``w`` at ``layer``.
+__device__ __forceinline__ uint8_t* staging_addr(const Store& s, int w, int layer, int kvh) {
+  return w < s.S_p ? s.staging + (((int64_t)w * s.L + layer) * 2 * s.H + kvh) * kRawRecord
+                   : s.scratch + ((int64_t)(w - s.S_p) * 2 * s.H + kvh) * kRawRecord;
+}
+
+// Overflow slot allocator over a bitmap (set = in use), safe against a
+// concurrent allocator on another stream.  Returns -1 when full.
+__device__ int ovf_alloc(const Store& s, uint32_t hint) {
+  for (int i = 0; i < s.ovf_words; ++i) {
+    const int w = (int)((hint + (uint32_t)i) % (uint32_t)s.ovf_words);
+    uint32_t cur = __hip_atomic_load(&s.ovf_bits[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (cur != 0xffffffffu) {
+      const int bit = __builtin_ctz(~cur);
+      const uint32_t prev = atomicOr(&s.ovf_bits[w], 1u << bit);
+      if (!(prev & (1u << bit))) return 32 * w + bit;
+      cur = prev | (1u << bit);
+    }
+  }
+  return -1;
+}
+
+__device__ __forceinline__ void ovf_free(const Store& s, int64_t addr) {
+  const int64_t off = addr - reinterpret_cast<int64_t>(s.ovf_base);
+  if (off < 0 || off >= s.ovf_bytes) return;
+  const int slot = (int)(off / kRawRecord);
+  atomicAnd(&s.ovf_bits[slot >> 5], ~(1u << (slot & 31)));
+}
+
+// ---------------------------------------------------------------------------
+// prepare: one workgroup, phases separated by barriers (hbm_kv.cu:110-219):
+// GC of unreferenced staging, close marks (offset 127), claims (offset 0)
+// with transient / heir slots, the close list with heirs paired to donors,
+// then claimed blocks' records pointed at their staging.
+__global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const int64_t* slots, int n_tok,
+                                                               const int32_t* live, int n_live, int32_t step) {
+  const int tid = threadIdx.x;
+  int32_t* live_tag = s.tags + kTagLive * s.NB;
+  int32_t* close_tag = s.tags + kTagClose * s.NB;
+  int32_t* claim_tag = s.tags + kTagClaim * s.NB;
+  int32_t* dedupe_tag = s.tags + kTagCloseDedupe * s.NB;
+  if (tid == 0) {
+    s.counters[kTrans] = 0;
+    s.counters[kClaims] = 0;
+    s.counters[kCloses] = 0;
+    s.counters[kHeirs] = 0;
+    s.counters[kDonors] = 0;
+  }
+  for (int i = tid; i < n_live; i += kPrepThreads) live_tag[live[i]] = step;
+  __syncthreads();
+  for (int b = tid; b < s.NB; b += kPrepThreads) {
+    const int w = s.wslot[b];
+    if (w >= s.S_p) {
+      s.wslot[b] = -1;  // transient slots never outlive their step
+    } else if (w >= 0 && live_tag[b] != step) {
+      s.wslot[b] = -1;
+      s.free_stack[atomicAdd(&s.counters[kFreeTop], 1)] = w;
+    }
+  }
+  for (int i = tid; i < n_tok; i += kPrepThreads) {
+    const int64_t sl = slots[i];
+    if (sl >= 0 && (sl & 127) == 127) close_tag[sl >> 7] = step;
+  }
+  __syncthreads();
+  for (int i = tid; i < n_tok; i += kPrepThreads) {
+    const int64_t sl = slots[i];
+    if (sl < 0 || (sl & 127) != 0) continue;
+    const int b = (int)(sl >> 7);
+    if (atomicExch(&claim_tag[b], step) == step) continue;
+    int w = s.wslot[b];
+    if (w < 0) {
+      const bool closes = close_tag[b] == step;
+      if (closes) {  // opens and closes within the step: transient slot
+        const int t = atomicAdd(&s.counters[kTrans], 1);
+        if (t < s.S_t) w = s.S_p + t;
+      }
+      if (w < 0) {
+        const int top = atomicSub(&s.counters[kFreeTop], 1) - 1;
+        if (top >= 0) {
+          w = s.free_stack[top];
+        } else {
+          atomicAdd(&s.counters[kFreeTop], 1);
+          // No free persistent slot: stage in transient scratch and inherit
+          // the slot of a block closing this step.
+          const int t = closes ? s.S_t : atomicAdd(&s.counters[kTrans], 1);
+          if (t < s.S_t) {
+            w = s.S_p + t;
+            s.claim_list[s.cap + atomicAdd(&s.counters[kHeirs], 1)] = b;
+          } else {
+            atomicAdd(&s.counters[kErrStaging], 1);
+          }
+        }
+      }
+    }
+    s.wslot[b] = w;
+    if (w >= 0) s.claim_list[atomicAdd(&s.counters[kClaims], 1)] = b;
+  }
+  __syncthreads();
+  const int n_heirs = s.counters[kHeirs];
+  for (int i = tid; i < n_tok; i += kPrepThreads) {
+    const int64_t sl = slots[i];
+    if (sl < 0 || (sl & 127) != 127) continue;
+    const int b = (int)(sl >> 7);
+    if (atomicExch(&dedupe_tag[b], step) == step) continue;
+    const int w = s.wslot[b];
+    if (w < 0) continue;
+    const int c = atomicAdd(&s.counters[kCloses], 1);
+    s.close_list[c] = b;
+    int heir = -1;
+    if (w < s.S_p && n_heirs) {
+      const int d = atomicAdd(&s.counters[kDonors], 1);
+      if (d < n_heirs) heir = s.claim_list[s.cap + d];
+    }
+    s.close_list[s.cap + c] = heir;
+  }
+  __syncthreads();
+  if (tid == 0 && s.counters[kDonors] < n_heirs) atomicAdd(&s.counters[kErrStaging], n_heirs - s.counters[kDonors]);
+  const int n_claim = s.counters[kClaims];
+  const int per = s.L * 2 * s.H;
+  for (int x = tid; x < n_claim * per; x += kPrepThreads) {
+    const int b = s.claim_list[x / per];
+    const int r = x % per, layer = r / (2 * s.H), kvh = r % (2 * s.H);
+    const int64_t idx = ((int64_t)layer * s.NB + b) * 2 * s.H + kvh;
+    ovf_free(s, s.rec_addr[idx]);
+    s.rec_addr[idx] = reinterpret_cast<int64_t>(staging_addr(s, s.wslot[b], layer, kvh));
+    s.rec_len[idx] = kRawVarLen;
+    if (kvh == 0) s.fill[(int64_t)layer * s.NB + b] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// write: one wavefront per (token, head).  Lane p (0..63) moves the dim pair
+// (2p, 2p+1) of K (one u32: both scalars are in the same kernel-order word)
+// and of V (two u16: a V pair belongs to two threads) into the raw
+// kernel-order staging record.
+__global__ void __launch_bounds__(kThreads) write_kernel(Store s, const uint16_t* k, const uint16_t* v, int64_t ks0,
+                                                        int64_t ks1, int64_t vs0, int64_t vs1, const int64_t* slots,
+                                                        int n, int layer) {
+  const int item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (item >= n * s.H) return;
+  const int tok = item / s.H, h = item % s.H;
+  const int64_t sl = slots[tok];
+  if (sl < 0) return;
+  const int b = (int)(sl >> 7), off = (int)(sl & 127);
+  const int w = s.wslot[b];
+  if (w < 0) return;
+  const int p = threadIdx.x & 63;
+  {
+    const uint32_t val = *reinterpret_cast<const uint32_t*>(k + tok * ks0 + h * ks1 + 2 * p);
+    // K: token off = 16 tw + 8 j + g, dim 2p = 16 st + 8 f + 2 c
+    const int st = p >> 3, f = (p >> 2) & 1, c = p & 3;
+    const int tw = off >> 4, j = (off >> 3) & 1, g = off & 7;
+    const int t = 32 * tw + 4 * g + c;
+    uint8_t* rec = staging_addr(s, w, layer, h);
+    *reinterpret_cast<uint32_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f)) = val;
+  }
+  {
+    const uint32_t val = *reinterpret_cast<const uint32_t*>(v + tok * vs0 + h * vs1 + 2 * p);
+    // V: token off = 16 st + 8 f + 2 c + e, dim d = 16 tw + 8 j + g
+    const int st = off >> 4, f = (off >> 3) & 1, c = (off >> 1) & 3, e = off & 1;
+    uint8_t* rec = staging_addr(s, w, layer, s.H + h);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int d = 2 * p + q;
+      const int tw = d >> 4, j = (d >> 3) & 1, g = d & 7;
+      const int t = 32 * tw + 4 * g + c;
+      *reinterpret_cast<uint16_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f + e)) = (uint16_t)(val >> (16 * q));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Record encoder core: one 256-thread workgroup, thread t holding the 8
+// kernel-order words of thread t.  Computes codes, counts, the variable
+// region (in LDS) and whether the record codes.
+
+struct EncShared {
+  uint8_t rank[256];
+  uint32_t var32[kVarCap / 4];
+  int wsum[2][8];  // per 32-thread slab: escapes, raws
+  int s_off, s_ovf;
+};
+
+struct EncResult {
+  bool codes;
+  int var_len;
+  int raw_offset;
+  int etot, rtot;
+};
+
+// Per-thread symbol words, escape / raw masks; then totals across the
+// workgroup.  Leaves the escape/raw exclusive prefixes of this thread in
+// eo / ro.
+__device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared& sh, uint32_t (&sym)[6],
+                                                 uint64_t& emask, uint64_t& rmask, int& eo, int& ro) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) sym[i] = 0;
+  emask = 0;
+  rmask = 0;
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sc = 8 * st + e, gi = sc >> 5, sg = sc & 31;
+      const uint32_t val = (u4(wd[st], e >> 1) >> (16 * (e & 1))) & 0xffffu;
+      const int r = sh.rank[val >> 8];
+      const uint32_t code = r < kPrimaryDirect ? (uint32_t)r : (uint32_t)kPrimaryDirect;
+      if (sg < 24) {
+        sym[3 * gi + (sg >> 3)] |= code << (4 * (sg & 7));
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 3; ++kk) sym[3 * gi + kk] |= ((code >> kk) & 1u) << (4 * (sg - 24) + 3);
+      }
+      if (r >= kPrimaryDirect) emask |= 1ull << sc;
+      if (r >= kTableEntries) rmask |= 1ull << sc;
+    }
+  }
+  const int ne = __popcll(emask), nr = __popcll(rmask);
+  const int ei = wave_incl_scan(ne), ri = wave_incl_scan(nr);
+  // per 32-thread slab totals (two per wavefront)
+  const int e31 = __shfl(ei, 31, 64), e63 = __shfl(ei, 63, 64);
+  const int r31 = __shfl(ri, 31, 64), r63 = __shfl(ri, 63, 64);
+  if (lane == 0) {
+    sh.wsum[0][2 * wave] = e31;
+    sh.wsum[0][2 * wave + 1] = e63 - e31;
+    sh.wsum[1][2 * wave] = r31;
+    sh.wsum[1][2 * wave + 1] = r63 - r31;
+  }
+  __syncthreads();
+  int ebase = 0, rbase = 0, etot = 0, rtot = 0, rmax = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    if (w < 2 * wave) {
+      ebase += sh.wsum[0][w];
+      rbase += sh.wsum[1][w];
+    }
+    etot += sh.wsum[0][w];
+    rtot += sh.wsum[1][w];
+    rmax = max(rmax, sh.wsum[1][w]);
+  }
+  eo = ebase + ei - ne;
+  ro = rbase + ri - nr;
+  EncResult res;
+  res.etot = etot;
+  res.rtot = rtot;
+  res.raw_offset = (kHeaderBytes + ((etot + 1) >> 1) + 3) & ~3;
+  res.var_len = (res.raw_offset + 4 * rtot + 15) & ~15;
+  res.codes = res.var_len <= kVarCap && rmax <= kMaxWarpRaw;
+  return res;
+}
+
+// Builds the variable region in sh.var32 (coded records only).  Caller
+// zeroed sh.var32 before enc_analyse's barrier.
+__device__ __forceinline__ void enc_var(const uint4 (&wd)[8], EncShared& sh, const EncResult& res, uint64_t emask,
+                                        int eo, int ro) {
+  uint64_t m = emask;
+  while (m) {
+    const int sc = __builtin_ctzll(m);
+    m &= m - 1;
+    const int st = sc >> 3, e = sc & 7;
+    uint4 w = wd[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i)
+      if (st == i) w = wd[i];
+    const uint32_t high = ((u4(w, e >> 1) >> (16 * (e & 1))) >> 8) & 0xffu;
+    const int r = sh.rank[high];
+    const uint32_t nib = r < kTableEntries ? (uint32_t)(r - kPrimaryDirect) : (uint32_t)kRawNibble;
+    const int bit = 8 * kHeaderBytes + 4 * eo;
+    atomicOr(&sh.var32[bit >> 5], nib << (bit & 31));
+    if (r >= kTableEntries) sh.var32[(res.raw_offset >> 2) + ro++] = (uint32_t)eo | (high << 16);
+    ++eo;
+  }
+  if (threadIdx.x == 0) {
+    sh.var32[0] = res.etot;
+    sh.var32[1] = res.rtot;
+    sh.var32[2] = res.raw_offset;
+    sh.var32[3] = 0;
+    int ep = 0, rp = 0;
+    for (int w = 0; w < 8; ++w) {
+      const int e16 = ep & 0xFFFF, r16 = rp & 0xFFFF;
+      // u16 esc_prefix[8] at byte 16, raw_prefix[8] at byte 32
+      if (w & 1) {
+        sh.var32[4 + (w >> 1)] |= (uint32_t)e16 << 16;
+        sh.var32[8 + (w >> 1)] |= (uint32_t)r16 << 16;
+      } else {
+        sh.var32[4 + (w >> 1)] = (uint32_t)e16;
+        sh.var32[8 + (w >> 1)] = (uint32_t)r16;
+      }
+      ep += sh.wsum[0][w];
+      rp += sh.wsum[1][w];
+    }
+  }
+}
+
+// Writes a coded record (dense part from registers, variable part from LDS)
+// at ``dst`` (16-byte aligned).
+__device__ __forceinline__ void enc_store(uint8_t* dst, const uint4 (&wd)[8], const uint32_t (&sym)[6],
+                                          const EncShared& sh, int var_len) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint4 a = wd[2 * j], c = wd[2 * j + 1];
+    // low bytes of the 16 scalars of chunk j
+    *reinterpret_cast<uint4*>(dst + 16 * (256 * j + tid)) =
+        make_uint4(perm(a.y, a.x, 0x06040200u), perm(a.w, a.z, 0x06040200u), perm(c.y, c.x, 0x06040200u),
+                   perm(c.w, c.z, 0x06040200u));
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+    *reinterpret_cast<uint2*>(dst + kLowBytes + 8 * (256 * m + tid)) = make_uint2(sym[2 * m], sym[2 * m + 1]);
+  for (int i = tid; i < var_len / 16; i += kThreads)
+    *reinterpret_cast<uint4*>(dst + kDenseBytes + 16 * i) = reinterpret_cast<const uint4*>(sh.var32)[i];
+}
+
+// grid (max_close, 2H): workgroup (i, kvh) encodes record kvh of
+// close_list[i] at ``layer`` from staging into the block's arena page (each
+// record takes the next kDenseBytes + var_len bytes, claimed by CAS on
+// fill), or raw into the overflow pool when it does not code or no longer
+// fits.  Also hands the slot's record to the block's heir (hbm_kv.cu:278-289).
+__global__ void __launch_bounds__(kThreads) encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes,
+                                                         const uint8_t* rank_of) {
+  __shared__ EncShared sh;
+  if ((int)blockIdx.x >= s.counters[kCloses]) return;
+  const int kvh = blockIdx.y, tid = threadIdx.x;
+  const int b = s.close_list[blockIdx.x];
+  uint8_t* src = staging_addr(s, s.wslot[b], layer, kvh);
+  const int64_t idx = ((int64_t)layer * s.NB + b) * 2 * s.H + kvh;
+  sh.rank[tid] = rank_of[((int64_t)layer * 2 * s.H + kvh) * 256 + tid];
+  for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
+  uint4 wd[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) wd[st] = ld16(src + 16 * (256 * st + tid));
+  const int heir = s.close_list[s.cap + blockIdx.x];
+  if (heir >= 0) {
+    const uint8_t* from = staging_addr(s, s.wslot[heir], layer, kvh);
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      *reinterpret_cast<uint4*>(src + 16 * (256 * st + tid)) = ld16(from + 16 * (256 * st + tid));
+    if (tid == 0) s.rec_addr[((int64_t)layer * s.NB + heir) * 2 * s.H + kvh] = reinterpret_cast<int64_t>(src);
+  }
+  __syncthreads();
+  uint32_t sym[6];
+  uint64_t emask, rmask;
+  int eo, ro;
+  const EncResult res = enc_analyse(wd, sh, sym, emask, rmask, eo, ro);
+  if (tid == 0) {
+    int off = -1;
+    if (res.codes) {
+      int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
+      const int need = kDenseBytes + res.var_len;
+      int cur = __hip_atomic_load(fill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      while (cur + need <= page_bytes) {
+        const int prev = atomicCAS(fill, cur, cur + need);
+        if (prev == cur) {
+          off = cur;
+          break;
+        }
+        cur = prev;
+      }
+      if (off < 0) atomicAdd(&s.counters[kSpills], 1);
+    }
+    sh.s_off = off;
+  }
+  __syncthreads();
+  if (sh.s_off < 0) {
+    if (tid == 0) {
+      const int slot = ovf_alloc(s, (uint32_t)(b * 2 * s.H + kvh));
+      if (slot < 0) atomicAdd(&s.counters[kErrOverflow], 1);
+      atomicAdd(&s.counters[kFallbacks], 1);
+      atomicAdd(&s.counters[kEncoded], 1);
+      sh.s_ovf = slot;
+    }
+    __syncthreads();
+    if (sh.s_ovf < 0) return;  // record stays in staging (data loss is counted)
+    uint8_t* dst = s.ovf_base + (int64_t)sh.s_ovf * kRawRecord;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) *reinterpret_cast<uint4*>(dst + 16 * (256 * st + tid)) = wd[st];
+    if (tid == 0) {
+      s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
+      s.rec_len[idx] = kRawVarLen;
+    }
+    return;
+  }
+  enc_var(wd, sh, res, emask, eo, ro);
+  __syncthreads();
+  uint8_t* dst = arena + (int64_t)b * page_bytes + sh.s_off;
+  enc_store(dst, wd, sym, sh, res.var_len);
+  if (tid == 0) {
+    s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
+    s.rec_len[idx] = res.var_len;
+    atomicAdd(&s.counters[kEncoded], 1);
+  }
+}
+
+// Closed blocks release their staging or pass it to their heir; the close
+// count is reset so a forward without a fresh prepare encodes nothing.
+__global__ void __launch_bounds__(kThreads) commit_kernel(Store s) {
+  const int n = s.counters[kCloses];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int b = s.close_list[i];
+    const int w = s.wslot[b];
+    const int heir = s.close_list[s.cap + i];
+    if (heir >= 0)
+      s.wslot[heir] = w;
+    else if (w >= 0 && w < s.S_p)
+      s.free_stack[atomicAdd(&s.counters[kFreeTop], 1)] = w;
+    s.wslot[b] = -1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) s.counters[kCloses] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Decode of whole records into token-major BF16 (gather / batch decode).
+// One 256-thread workgroup per record: wave W decodes slab W (kernel-order
+// threads 64W..64W+63, lane = thread) into an LDS tile [128 tok][128 dim],
+// then the tile is stored with 16-byte coalesced writes.
+
+constexpr int kTileRow = 256;  // bytes per token row in the tile
+struct DecShared {
+  uint8_t tile[kTokens * kTileRow];
+  uint8_t esc[4][kEscLds];
+};
+
+__device__ __forceinline__ int tile_off(int tok, int dim) {
+  // 16-byte chunk of the row swizzled by the token so that the column
+  // writes of V records spread over banks.
+  return tok * kTileRow + ((((dim >> 3) ^ (tok & 15)) & 15) << 4) + 2 * (dim & 7);
+}
+
+__device__ void decode_record_to_tile(const uint8_t* rec, int vlen, int kv, const HeadLut& lut, DecShared& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int w = tid >> 5, g = (tid >> 2) & 7, c = tid & 3;
+  auto put = [&](int st, const uint4& wd) {
+    const uint32_t d[4] = {wd.x, wd.y, wd.z, wd.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = i >> 1, f = i & 1;
+      const int row = 16 * w + 8 * j + g, col = 16 * st + 8 * f + 2 * c;
+      if (kv == 0) {
+        *reinterpret_cast<uint32_t*>(sh.tile + tile_off(row, col)) = d[i];
+      } else {
+        *reinterpret_cast<uint16_t*>(sh.tile + tile_off(col, row)) = (uint16_t)d[i];
+        *reinterpret_cast<uint16_t*>(sh.tile + tile_off(col + 1, row)) = (uint16_t)(d[i] >> 16);
+      }
+    }
+  };
+  auto emit = [&](auto st, const uint4& wd) { put(decltype(st)::value, wd); };
+  SlabBuf b;
+  const bool raw = vlen > kVarCap;
+  load_thread(rec, raw, tid, b);
+  if (raw) {
+    raw_words(b, rec, tid, emit);
+    return;
+  }
+  const uint8_t* var = rec + kDenseBytes;
+  auto rd4 = [&](int off) { return ld4(var + off); };
+  const SlabHdr h = slab_header(rd4, wave);
+  stage_escapes(rd4, h, lut.s, sh.esc[wave], lane);
+  const int cnt = thread_escapes(b);
+  const int incl = wave_incl_scan(cnt);
+  decode_words(b, sh.esc[wave], (h.e0 & 7) + incl - cnt, lut.p0, lut.p1, emit);
+}
+
+// Stores the tile: token row r to out + r * row_stride (bytes).
+__device__ __forceinline__ void store_tile(const DecShared& sh, uint8_t* out, int64_t row_stride) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int x = q * kThreads + threadIdx.x, r = x >> 4, jj = x & 15;
+    const uint4 val = *reinterpret_cast<const uint4*>(sh.tile + r * kTileRow + (((jj ^ (r & 15)) & 15) << 4));
+    *reinterpret_cast<uint4*>(out + r * row_stride + jj * 16) = val;
+  }
+}
+
+// grid (P, 2H): record kvh of block src[i] at one layer -> workspace page i.
+__global__ void __launch_bounds__(kThreads) gather_kernel(const int32_t* src, const int64_t* rec_addr,
+                                                         const int32_t* rec_len, const uint32_t* plut,
+                                                         const uint8_t* slut, uint8_t* wk, uint8_t* wv, int H) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  DecShared& sh = *reinterpret_cast<DecShared*>(smem);
+  const int kvh = blockIdx.y, kv = kvh / H, h = kvh % H;
+  const int64_t idx = (int64_t)src[blockIdx.x] * 2 * H + kvh;
+  const uint8_t* rec = reinterpret_cast<const uint8_t*>(rec_addr[idx]);
+  decode_record_to_tile(rec, rec_len[idx], kv, load_lut(plut, slut, kvh), sh);
+  __syncthreads();
+  uint8_t* out = (kv == 0 ? wk : wv) + ((int64_t)blockIdx.x * kTokens * H + h) * kTileRow;
+  store_tile(sh, out, (int64_t)H * kTileRow);
+}
+
+// grid (n): record i (any table, K or V) -> out [i, 128, 128].
+__global__ void __launch_bounds__(kThreads) decode_records_kernel(const int64_t* rec_addr, const int32_t* rec_len,
+                                                                 const int32_t* kv, const uint32_t* plut,
+                                                                 const uint8_t* slut, const int32_t* tab_idx,
+                                                                 uint8_t* out) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  DecShared& sh = *reinterpret_cast<DecShared*>(smem);
+  const int i = blockIdx.x;
+  const uint8_t* rec = reinterpret_cast<const uint8_t*>(rec_addr[i]);
+  decode_record_to_tile(rec, rec_len[i], kv[i], load_lut(plut, slut, tab_idx[i]), sh);
+  __syncthreads();
+  store_tile(sh, out + (int64_t)i * kRawRecord, kTileRow);
+}
+
+// grid (n): token-major record i -> coded bytes in out row i, lens[i].
+__global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t* raw, const int32_t* kvs,
+                                                                 const uint8_t* rank_of, const int32_t* tab_idx,
+                                                                 uint8_t* out, int32_t* lens) {
+  __shared__ EncShared sh;
+  const int i = blockIdx.x, tid = threadIdx.x;
+  const int kv = kvs[i];
+  const uint16_t* src = raw + (int64_t)i * kTokens * kDim;
+  sh.rank[tid] = rank_of[(int64_t)tab_idx[i] * 256 + tid];
+  for (int x = tid; x < kVarCap / 4; x += kThreads) sh.var32[x] = 0;
+  // thread tid's kernel-order words from the token-major record
+  const int w = tid >> 5, g = (tid >> 2) & 7, c = tid & 3;
+  uint4 wd[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    uint32_t d[4];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int j = i4 >> 1, f = i4 & 1;
+      const int row = 16 * w + 8 * j + g, col = 16 * st + 8 * f + 2 * c;
+      if (kv == 0) {
+        d[i4] = *reinterpret_cast<const uint32_t*>(src + row * kDim + col);
+      } else {
+        d[i4] = (uint32_t)src[col * kDim + row] | ((uint32_t)src[(col + 1) * kDim + row] << 16);
+      }
+    }
+    wd[st] = make_uint4(d[0], d[1], d[2], d[3]);
+  }
+  __syncthreads();
+  uint32_t sym[6];
+  uint64_t emask, rmask;
+  int eo, ro;
+  const EncResult res = enc_analyse(wd, sh, sym, emask, rmask, eo, ro);
+  uint8_t* dst = out + (int64_t)i * kRawRecord;
+  if (!res.codes) {
+#pragma unroll
+    for (int st = 0; st < 8; ++st) *reinterpret_cast<uint4*>(dst + 16 * (256 * st + tid)) = wd[st];
+    if (tid == 0) lens[i] = kRawRecord;
+    return;
+  }
+  enc_var(wd, sh, res, emask, eo, ro);
+  __syncthreads();
+  enc_store(dst, wd, sym, sh, res.var_len);
+  if (tid == 0) lens[i] = kDenseBytes + res.var_len;
+}
+
+// ---------------------------------------------------------------------------
+// Block blobs (hbm_kv.cu:496-665): a 64-byte header (u32 magic, version, L,
+// H; i64 bytes, digest) and the i32 rec_len table [L, 2, H] in a 4096-padded
+// head, then the records in (layer, kv, head) order.
+constexpr uint32_t kBlobMagic = 0x424B5046u;  // "FPKB"
+constexpr uint32_t kBlobVersion = 1;
+constexpr int kBlobFixed = 64;
+constexpr int64_t kBlobAlign = 4096;
+constexpr int kMaxHeads = 16;
+enum : int { kBlobBadHeader = 1, kBlobBadLengths = 2, kBlobNoOverflow = 4 };
+
+__host__ __device__ __forceinline__ int64_t blob_head_bytes(int L, int H) {
+  return (kBlobFixed + 8LL * L * H + kBlobAlign - 1) / kBlobAlign * kBlobAlign;
+}
+
+__device__ long long block_sum(long long v, long long* red) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  long long t = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+// grid (n, L): workgroup (i, l) copies layer l's records of blocks[i].
+__global__ void __launch_bounds__(kThreads) blob_export_kernel(const int32_t* blocks, const int64_t* rec_addr,
+                                                              const int32_t* rec_len, uint8_t* out, int64_t stride,
+                                                              int64_t* lengths, int L, int H, int NB,
+                                                              int64_t digest) {
+  __shared__ long long red[kThreads / 64];
+  const int i = blockIdx.x, l = blockIdx.y, tid = threadIdx.x, per = 2 * H;
+  const int b = blocks[i];
+  long long before = 0, total = 0;
+  for (int g = tid; g < L * per; g += kThreads) {
+    const long long n = kDenseBytes + rec_len[((int64_t)(g / per) * NB + b) * per + g % per];
+    total += n;
+    if (g / per < l) before += n;
+  }
+  before = block_sum(before, red);
+  total = block_sum(total, red);
+  const int64_t head = blob_head_bytes(L, H);
+  uint8_t* dst = out + (int64_t)i * stride;
+  if (l == 0) {
+    if (tid == 0) {
+      uint32_t* h32 = reinterpret_cast<uint32_t*>(dst);
+      h32[0] = kBlobMagic;
+      h32[1] = kBlobVersion;
+      h32[2] = L;
+      h32[3] = H;
+      int64_t* h64 = reinterpret_cast<int64_t*>(dst + 16);
+      h64[0] = head + total;
+      h64[1] = digest;
+      lengths[i] = (head + total + kBlobAlign - 1) / kBlobAlign * kBlobAlign;
+    }
+    int32_t* table = reinterpret_cast<int32_t*>(dst + kBlobFixed);
+    for (int g = tid; g < L * per; g += kThreads) table[g] = rec_len[((int64_t)(g / per) * NB + b) * per + g % per];
+  }
+  int64_t off = head + before;
+  for (int kvh = 0; kvh < per; ++kvh) {
+    const int64_t idx = ((int64_t)l * NB + b) * per + kvh;
+    const int n = kDenseBytes + rec_len[idx];
+    const uint8_t* srcp = reinterpret_cast<const uint8_t*>(rec_addr[idx]);
+    for (int q = tid; q < n / 16; q += kThreads)
+      *reinterpret_cast<uint4*>(dst + off + 16 * q) = ld16(srcp + 16 * q);
+    off += n;
+  }
+}
+
+// grid (n, L): validates blob i and installs its layer-l records into
+// blocks[i]: coded records packed into the block's arena page, raw ones
+// (and coded ones that no longer fit) in overflow slots.  A failing blob
+// sets status[i] and leaves the layer's tables untouched.
+__global__ void __launch_bounds__(kThreads) blob_import_kernel(Store s, const uint8_t* src, int64_t src_bytes,
+                                                              const int64_t* offsets, const int32_t* blocks,
+                                                              int32_t* status, const int64_t* arena_base,
+                                                              const int64_t* arena_stride, int64_t digest) {
+  __shared__ long long red[kThreads / 64];
+  __shared__ int64_t s_src[2 * kMaxHeads], s_dst[2 * kMaxHeads];
+  __shared__ int s_fail;
+  const int i = blockIdx.x, l = blockIdx.y, tid = threadIdx.x, L = s.L, per = 2 * s.H;
+  const int b = blocks[i];
+  const int64_t off = offsets[i], head = blob_head_bytes(L, s.H);
+  if (off < 0 || off % 16 || off + head > src_bytes) {
+    if (tid == 0) atomicOr(&status[i], kBlobBadHeader);
+    return;
+  }
+  const uint8_t* blob = src + off;
+  const uint32_t* h32 = reinterpret_cast<const uint32_t*>(blob);
+  const int64_t* h64 = reinterpret_cast<const int64_t*>(blob + 16);
+  const int64_t declared = h64[0];
+  if (h32[0] != kBlobMagic || h32[1] != kBlobVersion || (int)h32[2] != L || (int)h32[3] != s.H ||
+      h64[1] != digest || declared < head || off + declared > src_bytes) {
+    if (tid == 0) atomicOr(&status[i], kBlobBadHeader);
+    return;
+  }
+  const int32_t* table = reinterpret_cast<const int32_t*>(blob + kBlobFixed);
+  long long before = 0, total = 0;
+  int bad = 0;
+  for (int g = tid; g < L * per; g += kThreads) {
+    const int v = table[g];
+    const bool ok = v == kRawVarLen || (v >= kHeaderBytes && v <= kVarCap && v % 16 == 0);
+    bad |= !ok;
+    const long long n = kDenseBytes + (ok ? v : 0);
+    total += n;
+    if (g / per < l) before += n;
+  }
+  bad = __syncthreads_or(bad);
+  before = block_sum(before, red);
+  total = block_sum(total, red);
+  if (bad || head + total != declared) {
+    if (tid == 0) atomicOr(&status[i], kBlobBadLengths);
+    return;
+  }
+  const int32_t* lens = table + l * per;
+  if (tid == 0) {
+    const int64_t page = arena_stride[l];
+    const int64_t page_ptr = arena_base[l] + (int64_t)b * page;
+    int64_t from = head + before;
+    int fill = 0, placed = 0;
+    for (; placed < per; ++placed) {
+      const int n = kDenseBytes + lens[placed];
+      int64_t d;
+      if (lens[placed] != kRawVarLen && fill + n <= page) {
+        d = page_ptr + fill;
+        fill += n;
+      } else {
+        const int slot = ovf_alloc(s, (uint32_t)(b * per + placed));
+        if (slot < 0) break;
+        d = reinterpret_cast<int64_t>(s.ovf_base) + (int64_t)slot * kRawRecord;
+      }
+      s_src[placed] = from;
+      s_dst[placed] = d;
+      from += n;
+    }
+    s_fail = placed < per;
+    if (s_fail) {
+      for (int k = 0; k < placed; ++k) ovf_free(s, s_dst[k]);
+      atomicOr(&status[i], kBlobNoOverflow);
+    } else {
+      s.fill[(int64_t)l * s.NB + b] = fill;
+    }
+  }
+  __syncthreads();
+  if (s_fail) return;
+  for (int kvh = 0; kvh < per; ++kvh) {
+    const uint8_t* from = blob + s_src[kvh];
+    uint8_t* to = reinterpret_cast<uint8_t*>(s_dst[kvh]);
+    for (int q = tid; q < (kDenseBytes + lens[kvh]) / 16; q += kThreads)
+      *reinterpret_cast<uint4*>(to + 16 * q) = *reinterpret_cast<const uint4*>(from + 16 * q);
+  }
+  __syncthreads();
+  if (tid < per) {
+    const int64_t idx = ((int64_t)l * s.NB + b) * per + tid;
+    ovf_free(s, s.rec_addr[idx]);
+    s.rec_addr[idx] = s_dst[tid];
+    s.rec_len[idx] = lens[tid];
+  }
+}
+
+}  // namespace
+}  // namespace fp
+
+using namespace fp;
+
+extern "C" int fp_hbm_prepare(const fp_store_t* d, const int64_t* slot_mapping, int64_t n_tok, const int32_t* live,
+                              int64_t n_live, int64_t step, fp_stream_t stream) {
+  if (check_store(d)) return -1;
+  FP_CHECK(n_tok >= 0 && n_live >= 0, "negative token or live count");
+  FP_CHECK(2 * n_tok <= 2 * d->list_cap, "block lists too small");
+  FP_CHECK(n_live <= d->num_blocks, "more live blocks than blocks");
+  const Store s = make_store(d);
+  hipLaunchKernelGGL(prepare_kernel, dim3(1), dim3(kPrepThreads), 0, stream, s, slot_mapping, (int)n_tok, live,
+                     (int)n_live, (int32_t)step);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_hbm_write(const fp_store_t* d, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+                            int64_t v_s0, int64_t v_s1, const int64_t* slot_mapping, int64_t n, int64_t layer,
+                            fp_stream_t stream) {
+  if (n == 0) return 0;
+  if (check_store(d)) return -1;
+  FP_CHECK(n > 0 && layer >= 0 && layer < d->num_layers, "bad token count or layer");
+  FP_CHECK(k_s0 % 2 == 0 && k_s1 % 2 == 0 && v_s0 % 2 == 0 && v_s1 % 2 == 0,
+           "K/V strides must keep dim pairs 4-byte aligned");
+  const Store s = make_store(d);
+  const int64_t items = n * d->kv_heads;
+  const int64_t grid = (items + kThreads / 64 - 1) / (kThreads / 64);
+  FP_CHECK(grid < (1LL << 31), "too many tokens");
+  hipLaunchKernelGGL(write_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s,
+                     static_cast<const uint16_t*>(key), static_cast<const uint16_t*>(value), k_s0, k_s1, v_s0, v_s1,
+                     slot_mapping, (int)n, (int)layer);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_hbm_encode(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
+                             int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream) {
+  if (max_close == 0) return 0;
+  if (check_store(d)) return -1;
+  FP_CHECK(max_close > 0 && max_close <= d->list_cap, "close list too small");
+  FP_CHECK(rank_of_elems == d->num_layers * 2 * d->kv_heads * 256, "rank_of must hold every layer");
+  FP_CHECK(page_bytes % 16 == 0 && page_bytes > 0 && page_bytes < (1LL << 31), "bad arena page size");
+  FP_CHECK(layer >= 0 && layer < d->num_layers && arena % 16 == 0, "bad layer or arena address");
+  FP_CHECK(max_close < (1LL << 31), "too many closing blocks");
+  const Store s = make_store(d);
+  hipLaunchKernelGGL(encode_kernel, dim3((unsigned)max_close, (unsigned)(2 * d->kv_heads)), dim3(kThreads), 0,
+                     stream, s, (int)layer, reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_hbm_commit(const fp_store_t* d, fp_stream_t stream) {
+  if (check_store(d)) return -1;
+  const Store s = make_store(d);
+  hipLaunchKernelGGL(commit_kernel, dim3(1), dim3(kThreads), 0, stream, s);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+static int set_dec_smem() {
+  static bool done = false;
+  if (!done) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(gather_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecShared)) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(decode_records_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecShared)) != hipSuccess) {
+      set_error("cannot raise the decode kernels' LDS limit");
+      return -1;
+    }
+    done = true;
+  }
+  return 0;
+}
+
+extern "C" int fp_hbm_gather(const int32_t* src_blocks, int64_t n, const int64_t* rec_addr, const int32_t* rec_len,
+                             const uint32_t* plut, const uint8_t* slut, void* wk, void* wv, int64_t ws_bytes,
+                             int64_t kv_heads, fp_stream_t stream) {
+  if (n == 0) return 0;
+  FP_CHECK(n > 0 && kv_heads > 0 && kv_heads <= 64, "bad block count or kv_heads");
+  FP_CHECK(ws_bytes >= n * kTokens * kv_heads * kTileRow, "workspace too small");
+  FP_CHECK(n < (1LL << 31), "too many blocks");
+  if (set_dec_smem()) return -1;
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)n, (unsigned)(2 * kv_heads)), dim3(kThreads), sizeof(DecShared),
+                     stream, src_blocks, rec_addr, rec_len, plut, slut, static_cast<uint8_t*>(wk),
+                     static_cast<uint8_t*>(wv), (int)kv_heads);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_hbm_export(const int32_t* blocks, int64_t n, const int64_t* rec_addr, const int32_t* rec_len,
+                             int64_t num_layers, int64_t num_blocks, int64_t kv_heads, uint8_t* out,
+                             int64_t out_bytes, int64_t stride, int64_t* lengths, int64_t digest,
+                             fp_stream_t stream) {
+  if (n == 0) return 0;
+  FP_CHECK(n > 0 && num_layers > 0 && kv_heads > 0 && num_blocks > 0, "bad export geometry");
+  FP_CHECK(reinterpret_cast<uintptr_t>(out) % 16 == 0, "export buffer must be contiguous 16-byte aligned uint8");
+  FP_CHECK(stride % 16 == 0 &&
+               stride >= blob_head_bytes((int)num_layers, (int)kv_heads) + 2LL * num_layers * kv_heads * kRawRecord &&
+               out_bytes >= n * stride,
+           "export stride or buffer too small");
+  hipLaunchKernelGGL(blob_export_kernel, dim3((unsigned)n, (unsigned)num_layers), dim3(kThreads), 0, stream, blocks,
+                     rec_addr, rec_len, out, stride, lengths, (int)num_layers, (int)kv_heads, (int)num_blocks, digest);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_hbm_import(const fp_store_t* d, const uint8_t* src, int64_t src_bytes, const int64_t* offsets,
+                             const int32_t* blocks, int64_t n, int32_t* status, const int64_t* arena_base,
+                             const int64_t* arena_stride, int64_t digest, fp_stream_t stream) {
+  if (n == 0) return 0;
+  if (check_store(d)) return -1;
+  FP_CHECK(d->kv_heads <= kMaxHeads, "too many KV heads");
+  FP_CHECK(reinterpret_cast<uintptr_t>(src) % 16 == 0, "import buffer must be contiguous 16-byte aligned uint8");
+  const Store s = make_store(d);
+  hipLaunchKernelGGL(blob_import_kernel, dim3((unsigned)n, (unsigned)d->num_layers), dim3(kThreads), 0, stream, s,
+                     src, src_bytes, offsets, blocks, status, arena_base, arena_stride, digest);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_encode_records(const void* raw, int64_t n, const int32_t* kv, const uint8_t* rank_of,
+                                 const int32_t* tab_idx, int64_t n_tables, uint8_t* out, int32_t* lens,
+                                 fp_stream_t stream) {
+  if (n == 0) return 0;
+  FP_CHECK(n > 0 && n < (1LL << 31) && n_tables > 0, "bad record or table count");
+  hipLaunchKernelGGL(encode_records_kernel, dim3((unsigned)n), dim3(kThreads), 0, stream,
+                     static_cast<const uint16_t*>(raw), kv, rank_of, tab_idx, out, lens);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_decode_records(const int64_t* rec_addr, const int32_t* rec_len, int64_t n, const int32_t* kv,
+                                 const uint32_t* plut, const uint8_t* slut, const int32_t* tab_idx,
+                                 int64_t n_tables, void* out, fp_stream_t stream) {
+  if (n == 0) return 0;
+  FP_CHECK(n > 0 && n < (1LL << 31) && n_tables > 0, "bad record or table count");
+  if (set_dec_smem()) return -1;
+  hipLaunchKernelGGL(decode_records_kernel, dim3((unsigned)n), dim3(kThreads), sizeof(DecShared), stream, rec_addr,
+                     rec_len, kv, plut, slut, tab_idx, static_cast<uint8_t*>(out));
+  FP_LAUNCH_CHECK();
+  return 0;
+}

@@ -1,0 +1,143 @@
+"""Split-KV decode attention straight from FragPack KV records (MI355X).
+
+Reference: fragpack/ops/fused_attn_decode.py:41-219 (RecordTables,
+decode_units, workspace_elems, decode_attention, _launch) and
+fragpack/ops/fused_attn_decode.cu.
+
+One work unit handles a chunk of pages of one (sequence, KV head) pair for
+all query heads of the group, with an online softmax; a small combine kernel
+merges each sequence's chunks.  On gfx950 a unit is one 64-lane wavefront:
+it decodes each record in four passes straight into MFMA operands
+(``S^T = K Q^T`` and ``O^T += V^T P^T`` with v_mfma_f32_16x16x32_bf16, the
+group's query heads on the N side), so units never synchronise with each
+other.  A one-workgroup planner picks the chunk size on device once per step
+(``replan``) and every layer reuses it; the launch shape depends only on the
+batch size and ``units``, so the call is HIP-graph safe.
+
+Records are located through ``rec_addr[P, 2, H]`` (absolute device
+addresses) and ``rec_len[P, 2, H]`` (bytes past the dense part; raw records
+use ``RAW_VAR_LEN``).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from fragpack_amd.logging import init_logger
+from fragpack_amd.ops.fragpack_ext import extension
+
+logger = init_logger(__name__)
+
+GQA = 8
+# Work units per compute unit per KV head budget: a unit is one wavefront,
+# and the decode kernel runs 8 wavefronts per CU (2 per SIMD).
+WAVES_PER_CU = 8
+
+
+@dataclass(frozen=True)
+class RecordTables:
+    """One layer's record tables for :func:`decode_attention`.
+
+    Attributes:
+        rec_addr: int64 ``[P, 2, H]`` record device addresses.
+        rec_len: int32 ``[P, 2, H]`` record bytes minus ``DENSE_BYTES``.
+        plut: int32 ``[2, H, 2]`` primary tables.
+        slut: uint8 ``[2, H, 16]`` extended tables.
+    """
+
+    rec_addr: torch.Tensor
+    rec_len: torch.Tensor
+    plut: torch.Tensor
+    slut: torch.Tensor
+
+
+def decode_units(batch: int, kv_heads: int, num_sms: int) -> int:
+    """Work-unit capacity per KV head of a decode launch.
+
+    One unit per sequence plus one wave of split capacity minus one, as in
+    the reference (fused_attn_decode.py:58-85); a "wave" here is the
+    wavefronts the device runs at once per KV head: ``WAVES_PER_CU`` per
+    compute unit.  Depends only on the (padded) batch size, so the launch
+    shape is fixed under graph capture.
+
+    Args:
+        batch: Number of sequences (padded batch size under graphs).
+        kv_heads: KV heads per sequence.
+        num_sms: Compute-unit count (``multi_processor_count``; 256 on MI355X).
+
+    Returns:
+        Unit count, at least ``batch``.
+    """
+    wave = max(1, (WAVES_PER_CU * num_sms) // max(1, kv_heads))
+    return batch + wave - 1
+
+
+def workspace_elems(kv_heads: int, units: int) -> tuple[int, int, int]:
+    """Element counts of the ``(opart, ml, plan)`` workspace (float, float, int32)."""
+    rows = kv_heads * units * GQA
+    return rows * 128, rows * 2, 2 + 4 * units
+
+
+def decode_attention(
+    q: torch.Tensor,
+    tables: RecordTables,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float,
+    units: int,
+    out: torch.Tensor,
+    workspace: tuple[torch.Tensor, torch.Tensor, torch.Tensor],
+    replan: bool,
+) -> None:
+    """Split-KV decode attention for one query token per sequence.
+
+    Args:
+        q: BF16 ``[B, H * G, 128]`` queries (rows may be strided); G in 1, 2, 4, 8.
+        tables: Record tables of this layer.
+        block_table: int32 ``[B, max_pages]`` page ids (rows may be strided).
+        seq_lens: int32 ``[B]`` context lengths; 0 yields a zero output row.
+        scale: Softmax scale.
+        units: Work-unit capacity per KV head, at least ``B`` (e.g. from
+            :func:`decode_units`).
+        out: BF16 ``[B, H * G, 128]`` output (rows may be strided).
+        workspace: ``(opart, ml, plan)`` sized by :func:`workspace_elems`.
+        replan: Recompute the work plan from ``seq_lens`` and ``units``; later
+            layers of the same step may pass False.
+
+    Raises:
+        ValueError: If the query group does not divide ``GQA``.
+
+    Async/thread-safety:
+        Enqueues on the current stream; not synchronized.  Unlike the
+        reference, smaller groups run natively (no padded copies).
+    """
+    kv_heads = tables.rec_addr.shape[2]
+    group = q.shape[1] // kv_heads
+    if group * kv_heads != q.shape[1] or GQA % group:
+        raise ValueError(f"query heads {q.shape[1]} need a group dividing {GQA}")
+    _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, replan, group)
+
+
+def _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, replan, group=GQA) -> None:
+    extension().fused_decode(
+        q,
+        tables.rec_addr,
+        tables.rec_len,
+        tables.plut,
+        tables.slut,
+        block_table,
+        seq_lens,
+        workspace[0],
+        workspace[1],
+        workspace[2],
+        out,
+        units,
+        replan,
+        scale,
+        group,
+    )
+
+
+__all__ = ["GQA", "RecordTables", "decode_attention", "decode_units", "workspace_elems"]

@@ -1,0 +1,140 @@
+/*
+ * fragpack_hip.h -- C ABI of the MI355X FragPack hot path
+ * (libfragpack_hip.so, built from fragpack_amd/csrc/ for gfx950).
+ *
+ * Every entry point enqueues work on ``stream`` and returns without
+ * synchronising.  Return value: 0 on success, -1 on a rejected argument or a
+ * launch failure; fp_last_error() then holds the message (per host thread).
+ * All pointers are device pointers unless stated otherwise.  The library
+ * allocates no device memory.
+ *
+ * Each function replaces one function of the reference's pybind module
+ * (fragpack/ops/fragpack_ext.cpp:5-66), which the reference's Python layer
+ * calls with torch tensors; here the tensors are flattened to pointers,
+ * element strides and sizes.  The Python mirror
+ * (fragpack_amd/ops/fragpack_ext.py) keeps the reference's tensor signatures
+ * and calls these.
+ */
+#ifndef FRAGPACK_HIP_H_
+#define FRAGPACK_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* fp_stream_t; /* hipStream_t */
+
+/* The HBM store's state, i.e. the 13 tensors the reference passes to every
+ * hbm_* call, in its order (fragpack/ops/hbm_kv.py:287-301; struct Store in
+ * fragpack/ops/hbm_kv.cu:32-78), plus their geometry. */
+typedef struct fp_store {
+  int32_t* counters;   /* int32 [16]                                   */
+  int32_t* wslot;      /* int32 [NB] staging slot of an open block      */
+  int32_t* tags;       /* int32 [4, NB] per-block step stamps           */
+  int32_t* free_stack; /* int32 [S_p]                                   */
+  uint32_t* ovf_bits;  /* [ovf_words] overflow slots in use             */
+  int32_t* claim_list; /* int32 [2, list_cap]                           */
+  int32_t* close_list; /* int32 [2, list_cap]                           */
+  int64_t* rec_addr;   /* int64 [L, NB, 2, H] record device addresses  */
+  int32_t* rec_len;    /* int32 [L, NB, 2, H] bytes past the dense part */
+  uint8_t* staging;    /* [S_p, L, 2, H, 32768] persistent staging      */
+  uint8_t* scratch;    /* [S_t, 2, H, 32768] transient staging          */
+  uint8_t* overflow;   /* [O, 32768] raw overflow records               */
+  int32_t* fill;       /* int32 [L, NB] arena bytes used per page       */
+  int64_t num_layers, num_blocks, kv_heads;
+  int64_t staging_slots, scratch_slots, ovf_words, list_cap, overflow_records;
+} fp_store_t;
+
+/* Last error message of this host thread ("" if none). */
+const char* fp_last_error(void);
+/* ABI version (bumped on any signature change). */
+int fp_abi_version(void);
+
+/*
+ * Split-KV decode attention over FragPack records.
+ * Replaces fused_decode (fragpack/ops/fragpack_ext.cpp:5-9,
+ * fragpack/ops/fused_attn_decode.cu:429-478).
+ *   q           BF16 [B, H * group, 128], q_stride elements between rows
+ *   rec_addr    int64 [P, 2, H], rec_len int32 [P, 2, H] (one layer)
+ *   plut        uint32 [2, H, 2], slut uint8 [2, H, 16]
+ *   block_table int32 [B, bt_stride], seq_lens int32 [B]
+ *   opart/ml/plan  workspace (float, float, int32) of at least
+ *               H*units*8*128, H*units*16 and 2 + 4*units elements
+ *   out         BF16 [B, H * group, 128], out_stride elements between rows
+ *   group       query heads per KV head: 1, 2, 4 or 8 (the reference pads
+ *               smaller groups to 8 on the host; this kernel takes them as is)
+ */
+int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
+                    const int64_t* rec_addr, const int32_t* rec_len, const uint32_t* plut,
+                    const uint8_t* slut, const int32_t* block_table, int64_t bt_stride,
+                    const int32_t* seq_lens, float* opart, int64_t opart_elems, float* ml,
+                    int64_t ml_elems, int32_t* plan, int64_t plan_elems, void* out, int64_t out_stride,
+                    int64_t units, int replan, double scale, fp_stream_t stream);
+
+/* Step start: GC, staging claims, close list.  Replaces hbm_prepare
+ * (fragpack_ext.cpp:11-17, hbm_kv.cu:669-686). */
+int fp_hbm_prepare(const fp_store_t* s, const int64_t* slot_mapping, int64_t n_tok, const int32_t* live,
+                   int64_t n_live, int64_t step, fp_stream_t stream);
+
+/* New K/V tokens into kernel-order staging.  key/value BF16 [n, H, 128]
+ * with element strides (k_s0, k_s1), (v_s0, v_s1); head dim contiguous.
+ * Replaces hbm_write (fragpack_ext.cpp:19-25, hbm_kv.cu:688-705). */
+int fp_hbm_write(const fp_store_t* s, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+                 int64_t v_s0, int64_t v_s1, const int64_t* slot_mapping, int64_t n, int64_t layer,
+                 fp_stream_t stream);
+
+/* Encode this layer's records of the blocks closed this step into their
+ * arena pages (rank_of uint8 [L, 2, H, 256]).  Replaces hbm_encode
+ * (fragpack_ext.cpp:27-33, hbm_kv.cu:707-723). */
+int fp_hbm_encode(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
+                  int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream);
+
+/* Release closed blocks' staging.  Replaces hbm_commit
+ * (fragpack_ext.cpp:35-39, hbm_kv.cu:725-734). */
+int fp_hbm_commit(const fp_store_t* s, fp_stream_t stream);
+
+/* Decode records of blocks src_blocks[i] (one layer's rec tables, [NB, 2, H])
+ * into token-major BF16 pages wk / wv [>= n, 128, H, 128] (ws_bytes each).
+ * Replaces hbm_gather (fragpack_ext.cpp:41-43, hbm_kv.cu:736-753). */
+int fp_hbm_gather(const int32_t* src_blocks, int64_t n, const int64_t* rec_addr, const int32_t* rec_len,
+                  const uint32_t* plut, const uint8_t* slut, void* wk, void* wv, int64_t ws_bytes,
+                  int64_t kv_heads, fp_stream_t stream);
+
+/* Closed blocks -> block blobs at out + i * stride; lengths int64 [n].
+ * Replaces hbm_export (fragpack_ext.cpp:45-46, hbm_kv.cu:755-774). */
+int fp_hbm_export(const int32_t* blocks, int64_t n, const int64_t* rec_addr, const int32_t* rec_len,
+                  int64_t num_layers, int64_t num_blocks, int64_t kv_heads, uint8_t* out, int64_t out_bytes,
+                  int64_t stride, int64_t* lengths, int64_t digest, fp_stream_t stream);
+
+/* Validate and install block blobs (src, src_bytes) at offsets[i] into
+ * blocks[i]; status int32 [n] gets failure bits.  arena_base / arena_stride
+ * int64 [L].  Replaces hbm_import (fragpack_ext.cpp:48-55,
+ * hbm_kv.cu:776-802). */
+int fp_hbm_import(const fp_store_t* s, const uint8_t* src, int64_t src_bytes, const int64_t* offsets,
+                  const int32_t* blocks, int64_t n, int32_t* status, const int64_t* arena_base,
+                  const int64_t* arena_stride, int64_t digest, fp_stream_t stream);
+
+/*
+ * Batch record codec (device): the GPU form of the reference's CPU codec
+ * attn_page.encode_record / decode_record (fragpack/compression/
+ * attn_page.py:146-269), byte-identical to it.
+ *   fp_encode_records: raw BF16 token-major [n, 128, 128] -> out [n, 32768]
+ *     (record i in the first lens[i] bytes of row i); kv[i] in {0, 1};
+ *     rank_of uint8 [n_tables, 256], tab_idx[i] selects the table.
+ *   fp_decode_records: records (rec_addr[i], DENSE + rec_len[i] bytes) ->
+ *     token-major [n, 128, 128]; plut [n_tables, 2], slut [n_tables, 16].
+ */
+int fp_encode_records(const void* raw, int64_t n, const int32_t* kv, const uint8_t* rank_of,
+                      const int32_t* tab_idx, int64_t n_tables, uint8_t* out, int32_t* lens,
+                      fp_stream_t stream);
+int fp_decode_records(const int64_t* rec_addr, const int32_t* rec_len, int64_t n, const int32_t* kv,
+                      const uint32_t* plut, const uint8_t* slut, const int32_t* tab_idx, int64_t n_tables,
+                      void* out, fp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRAGPACK_HIP_H_ */
