@@ -1,0 +1,365 @@
+"""FragPack hot-path benchmark on one MI355X.
+
+Default workload: one attention layer, batch 4, 4 KV
+heads, 32 query heads (GQA 8), head_dim 128, every sequence at 8192 context
+(64 full compressed 128-token blocks each).  K/V are synthetic BF16 drawn
+N(0,1) x per-channel lognormal(0, 0.5) scale with 2% outlier channels x8;
+codec tables are calibrated (fragpack_amd.compression.attn_tables.calibrate)
+from a seeded [64, 1, 2, 128, H, 128] dump drawn the same way; the KV is
+written and encoded through the store's own path (prepare / write / encode /
+commit); Q ~ N(0,1) BF16.
+
+A step = one decode step of the layer: plan + fused decode attention (the
+merge is fused into the attention kernel).  ``value`` is the effective
+BF16-KV throughput (2 * sum(ceil(len/128)) * 128 * H * 128 * 2 bytes per
+step / step time), the reference benchmark's convention
+(benchmarks/fragpack_step_bench.py:320).  Extra fields report us/step, the
+compressed-byte rate, the roofline of the attention kernel (algorithmic
+compressed bytes per launch / its HIP-event time), the encoder leg (BASELINE
+config 3 shape) and the CPU oracle baseline.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+T = 128
+D = 128
+HBM_PEAK_GBS = 8000.0
+DENSE = 22528
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def channel_scales(rng, heads: int, outlier: float) -> np.ndarray:
+    """[2, H, 128] per-channel scales: lognormal(0, 0.5), outliers x8."""
+    s = rng.lognormal(0.0, 0.5, (2, heads, D))
+    s[rng.random((2, heads, D)) < outlier] *= 8.0
+    return s
+
+
+def calibrated_tables(rng, heads: int, scales: np.ndarray):
+    from fragpack_amd.compression.attn_tables import calibrate
+
+    dump = np.empty((64, 1, 2, T, heads, D), np.uint16)
+    for kv in range(2):
+        for h in range(heads):
+            dump[:, 0, kv, :, h, :] = bf16_bits(rng.standard_normal((64, T, D)) * scales[kv, h])
+    return calibrate(dump)  # [1, 2, H, 22]
+
+
+def gen_kv(torch, gen, n_tok: int, heads: int, scales_t, heavy: float = 0.0):
+    """BF16 [2, n_tok, H, 128] on the GPU; ``heavy`` of the values replaced by
+    Student-t(2) x 16 (config 3)."""
+    x = torch.randn((2, n_tok, heads, D), generator=gen, device="cuda") * scales_t[:, None]
+    if heavy > 0:
+        z = torch.randn((2, n_tok, heads, D), generator=gen, device="cuda")
+        chi = torch.randn((2, n_tok, heads, D, 2), generator=gen, device="cuda").pow(2).sum(-1)
+        t2 = z / torch.sqrt(chi / 2) * 16
+        pick = torch.rand((2, n_tok, heads, D), generator=gen, device="cuda") < heavy
+        x = torch.where(pick, t2, x)
+    return x.to(torch.bfloat16)
+
+
+def build_store(torch, heads: int, n_blocks: int, tables, gen, scales_t, fill_blocks: int, heavy: float = 0.0,
+                overflow: int = 8192, keep_kv: bool = False):
+    """A one-layer store whose blocks 0..n_blocks-1 are written and encoded."""
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+
+    dev = torch.device("cuda")
+    arena = torch.empty((n_blocks, page_bytes(heads)), dtype=torch.uint8, device=dev)
+    store = HbmKvStore([arena], heads, device_tables(tables, dev), max_tokens=fill_blocks * T, staging_slots=1,
+                       overflow_records=overflow)
+    kept = []
+    no_live = np.zeros(0, np.int32)
+    for b0 in range(0, n_blocks, fill_blocks):
+        n = min(fill_blocks, n_blocks - b0)
+        slots = (torch.arange(b0, b0 + n, device=dev)[:, None] * T + torch.arange(T, device=dev)).reshape(-1)
+        kv = gen_kv(torch, gen, n * T, heads, scales_t, heavy)
+        store.prepare(slots, slots.numel(), no_live)
+        store.write(0, kv[0], kv[1], slots)
+        store.encode(0, n)
+        store.commit()
+        if keep_kv:
+            kept.append(kv)
+    torch.cuda.synchronize()
+    return store, arena, (torch.cat(kept, dim=1) if keep_kv else None)
+
+
+def reference_decode(torch, q, kv, block_table, lens, heads, group, scale):
+    """fp32 torch attention over token-major KV [2, NB*128, H, 128]."""
+    out = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
+    kvf = kv.float().view(2, -1, T, heads, D)
+    for b in range(q.shape[0]):
+        n = int(lens[b])
+        pages = block_table[b, : math.ceil(n / T)].long().to(q.device)
+        k = kvf[0, pages].reshape(-1, heads, D)[:n]
+        v = kvf[1, pages].reshape(-1, heads, D)[:n]
+        qb = q[b].float().view(heads, group, D)
+        s = torch.einsum("hgd,thd->hgt", qb, k) * scale
+        out[b] = torch.einsum("hgt,thd->hgd", s.softmax(-1), v).reshape(heads * group, D)
+    return out
+
+
+def decode_bench(torch, args) -> dict:
+    from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
+
+    B, H, G, ctx = args.batch, args.heads, args.group, args.context
+    rng = np.random.default_rng(args.seed)
+    scales = channel_scales(rng, H, 0.02)
+    tables = calibrated_tables(rng, H, scales)
+    pages = math.ceil(ctx / T)
+    nb = B * pages
+    gen = torch.Generator(device="cuda").manual_seed(args.seed)
+    scales_t = torch.from_numpy(scales).float().cuda()
+    t0 = time.time()
+    store, arena, kv = build_store(torch, H, nb, tables, gen, scales_t, fill_blocks=64, keep_kv=True)
+    log(f"store filled: {nb} blocks x {2 * H} records in {time.time() - t0:.1f}s, stats {store.stats()}")
+    perm = torch.from_numpy(rng.permutation(nb).astype(np.int32)).cuda()
+    bt = perm.view(B, pages).contiguous()
+    lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    q = torch.randn((B, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    units = args.units or decode_units(B, H, sms)
+    opart, ml, plan = workspace_elems(H, units)
+    ws = (torch.empty(opart, device="cuda"), torch.empty(ml, device="cuda"),
+          torch.empty(plan, dtype=torch.int32, device="cuda"))
+    out = torch.empty_like(q)
+    tabs = RecordTables(*store.layer_tables(0))
+    scale = D ** -0.5
+
+    def step(replan=True):
+        decode_attention(q, tabs, bt, lens, scale, units, out, ws, replan)
+
+    # validation against an fp32 torch reference on the written KV
+    out.fill_(float("nan"))
+    step()
+    torch.cuda.synchronize()
+    ref = reference_decode(torch, q, kv, bt.cpu(), lens.cpu().numpy(), H, G, scale)
+    err = (out.float() - ref).abs()
+    tol = 2e-2 + 1e-2 * ref.abs()
+    valid = bool(torch.isfinite(out.float()).all() and (err <= tol).all())
+    log(f"validation vs fp32 reference: max abs err {err.max().item():.3e}, within 2e-2+1e-2*|ref|: {valid}")
+    del kv
+
+    # algorithmic bytes of one launch
+    rec_len = store.rec_len[0].cpu().numpy()  # [NB, 2, H]
+    used = bt.cpu().numpy()[:, :pages].reshape(-1)
+    rl = rec_len[used]  # [B*pages, 2, H]
+    rec_bytes = int(np.where(rl > 2048, 32768, DENSE + rl).sum())
+    meta_bytes = used.size * H * 24
+    qo_bytes = B * H * G * D * 2 * 2
+    algo_bytes = rec_bytes + meta_bytes + qo_bytes
+    eff_bytes = 2 * B * pages * T * H * D * 2
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step(True)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / args.steps
+    # the attention kernel alone (replan=False launches only attn_kernel)
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record(stream)
+    for _ in range(args.steps):
+        step(False)
+    k1.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = k0.elapsed_time(k1) / args.steps
+    comp_ratio = rec_bytes / (2 * used.size * H * 32768)
+    log(f"step {step_ms * 1e3:.1f} us, attn kernel {kern_ms * 1e3:.1f} us, "
+        f"compressed {rec_bytes / 1e6:.1f} MB ({comp_ratio:.3f} of raw), effective BF16 {eff_bytes / 1e6:.1f} MB")
+    return dict(step_ms=step_ms, kern_ms=kern_ms, algo_bytes=algo_bytes, eff_bytes=eff_bytes, rec_bytes=rec_bytes,
+                valid=valid, units=units, store=store, arena=arena, bt=bt, lens=lens, q=q, tables=tables,
+                scale=scale, comp_ratio=comp_ratio, max_err=err.max().item())
+
+
+def encode_bench(torch, args) -> dict:
+    """Store encode kernel over BASELINE config 3's shape: ``--encode-blocks``
+    completed blocks x 8 KV heads x K/V, 10% Student-t(2) x 16 values, an
+    8192-record overflow pool.  Times only the encode launches (fill and
+    overflow bitmap are reset between repetitions)."""
+    H = 8
+    n = args.encode_blocks
+    rng = np.random.default_rng(args.seed + 3)
+    scales = channel_scales(rng, H, 0.02)
+    tables = calibrated_tables(rng, H, scales)
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 3)
+    scales_t = torch.from_numpy(scales).float().cuda()
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+
+    # One step closes all n blocks: prepare once, write in chunks, then time
+    # the layer's encode launch.
+    arena = torch.empty((n, page_bytes(H)), dtype=torch.uint8, device="cuda")
+    store = HbmKvStore([arena], H, device_tables(tables, torch.device("cuda")), max_tokens=n * T,
+                       staging_slots=1, overflow_records=8192)
+    slots = torch.arange(n * T, device="cuda", dtype=torch.int64)
+    store.prepare(slots, slots.numel(), np.zeros(0, np.int32))
+    chunk = 2048 * T
+    for t0 in range(0, n * T, chunk):
+        t1 = min(n * T, t0 + chunk)
+        kv = gen_kv(torch, gen, t1 - t0, H, scales_t, heavy=0.1)
+        store.write(0, kv[0], kv[1], slots[t0:t1])
+        del kv
+    torch.cuda.synchronize()
+    ovf0 = store.ovf_bits.clone()
+    cnt0 = store.counters.clone()
+    addr0, len0 = store.rec_addr.clone(), store.rec_len.clone()
+    total = 0.0
+    reps = max(1, args.encode_reps)
+    for r in range(reps + 1):
+        store.fill.zero_()
+        store.ovf_bits.copy_(ovf0)
+        store.counters.copy_(cnt0)
+        store.rec_addr.copy_(addr0)
+        store.rec_len.copy_(len0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        store.encode(0, n)
+        e1.record()
+        torch.cuda.synchronize()
+        if r:  # first launch is warmup
+            total += e0.elapsed_time(e1)
+    ms = total / reps
+    c = store.counters.cpu().numpy()
+    rec_len = store.rec_len[0].cpu().numpy()
+    coded = rec_len <= 2048
+    written = int(np.where(coded, DENSE + rec_len, 32768).sum())
+    records = n * 2 * H
+    eff = records * 32768
+    log(f"encode: {records} records in {ms * 1e3:.0f} us -> {eff / ms / 1e6:.0f} GB/s effective, "
+        f"fallbacks {int(c[6])} (spills {int(c[8])}), overflow-full drops {int(c[5])}")
+    return dict(ms=ms, records=records, eff_bytes=eff, read_write_bytes=eff + written, fallbacks=int(c[6]),
+                spills=int(c[8]), err_overflow=int(c[5]))
+
+
+def cpu_baseline(torch, res, args) -> dict:
+    """The CPU oracle (C, OpenMP) on the same decode step: decode every record
+    of the 4 x 8192-token layer and run fp32 attention, timed on this host's
+    cores, repeated to ~``--cpu-seconds``."""
+    from oracle import oracle
+
+    store, arena = res["store"], res["arena"]
+    host_arena = arena.cpu().numpy().reshape(-1)
+    host_ovf = store.overflow.cpu().numpy().reshape(-1)
+    recs = np.concatenate([host_arena, host_ovf])
+    a_base, o_base = arena.data_ptr(), store.overflow.data_ptr()
+    addr = store.rec_addr[0].cpu().numpy()
+    in_ovf = (addr >= o_base) & (addr < o_base + host_ovf.size)
+    off = np.where(in_ovf, addr - o_base + host_arena.size, addr - a_base).astype(np.int64)
+    rec_len = store.rec_len[0].cpu().numpy()
+    q = res["q"].view(torch.int16).cpu().numpy().view(np.uint16)
+    bt = res["bt"].cpu().numpy()
+    lens = res["lens"].cpu().numpy()
+    tables = res["tables"][0]
+    threads = oracle.num_threads()
+    n, t0 = 0, time.time()
+    while True:
+        oracle.paged_attention(q, args.heads, recs, off, rec_len, tables, bt, lens, res["scale"], threads)
+        n += 1
+        if time.time() - t0 >= args.cpu_seconds:
+            break
+    per = (time.time() - t0) / n
+    return dict(value=round(res["eff_bytes"] / per / 1e9, 3), unit="GB/s (effective BF16 KV)", cores=threads,
+                kind="port", sample=f"{n} x the full config-1 step (4 seq x 4 KV heads x 8192 ctx, "
+                f"record decode + fp32 attention), {per * 1e3:.0f} ms each")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=4)
+    ap.add_argument("--heads", type=int, default=4)
+    ap.add_argument("--group", type=int, default=8)
+    ap.add_argument("--context", type=int, default=8192)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--units", type=int, default=0, help="override decode_units()")
+    ap.add_argument("--encode-blocks", type=int, default=32768)
+    ap.add_argument("--encode-reps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-encode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus N > 1 is not supported (see DESIGN.md, "
+                                   "'How the path would shard')"}))
+        sys.exit(2)
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(int(os.environ.get("LOCAL_RANK", "0")))
+    res = decode_bench(torch, args)
+    enc = None if args.no_encode else encode_bench(torch, args)
+    cpu = None if args.no_cpu else cpu_baseline(torch, res, args)
+    step_s = res["step_ms"] / 1e3
+    kern_s = res["kern_ms"] / 1e3
+    achieved = res["algo_bytes"] / kern_s / 1e9
+    line = {
+        "metric": "decode-attn effective BF16-KV GB/s (us/step, compressed GB/s, encode GB/s alongside)",
+        "value": round(res["eff_bytes"] / step_s / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["step_ms"], 5),
+        "us_per_step": round(res["step_ms"] * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codec + bf16 MFMA / fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) x lognormal channel scale, 2% outliers x8; calibrated tables)",
+        "config": {"workload": "config 1: decode step, B4 x H4 x G8 x 8192 ctx, head_dim 128, one layer",
+                   "batch": args.batch, "kv_heads": args.heads, "gqa": args.group, "context": args.context,
+                   "units": res["units"]},
+        "compressed_GBps": round(res["algo_bytes"] / step_s / 1e9, 2),
+        "compression": round(res["comp_ratio"], 4),
+        "validated": res["valid"],
+        "max_abs_err": res["max_err"],
+        "roofline": {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "us_per_launch": round(res["kern_ms"] * 1e3, 2),
+                     "algo_bytes_per_launch": res["algo_bytes"]},
+        "cpu_baseline": cpu,
+    }
+    if enc is not None:
+        line["encode"] = {"workload": f"config 3 shape: {args.encode_blocks} blocks x 8 KV heads x K/V, 10% "
+                                      "Student-t(2)x16, overflow 8192",
+                          "records": enc["records"], "us": round(enc["ms"] * 1e3, 1),
+                          "effective_GBps": round(enc["eff_bytes"] / enc["ms"] / 1e6, 1),
+                          "hbm_GBps": round(enc["read_write_bytes"] / enc["ms"] / 1e6, 1),
+                          "fallbacks": enc["fallbacks"], "spills": enc["spills"],
+                          "overflow_full_drops": enc["err_overflow"]}
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

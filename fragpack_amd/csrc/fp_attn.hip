@@ -5,22 +5,26 @@
 // Python contract fragpack/ops/fused_attn_decode.py:41-219.
 //
 // Design (MI355X):
-// * One work unit = one wavefront (64 lanes).  It walks a chunk of pages of
-//   one (sequence, KV head) with an online softmax; four independent
-//   wavefronts share a 256-thread workgroup and never synchronise with each
-//   other.  No block-level barrier appears in the page loop.
-// * Per page the wave decodes each record in four passes ("slabs" of 64
-//   kernel-order threads).  Lane l decodes kernel-order thread
-//   nt = 32 hh + 4 g + c of the slab, with c = l >> 4, hh = (l >> 3) & 1,
-//   g = l & 7.  With that assignment the decoded words are directly the A
-//   operands of v_mfma_f32_16x16x32_bf16: MFMA row = l % 16 indexes the token
-//   (K) or dim (V), and the four 16-lane groups (= c) hold four disjoint dim
-//   (K) or token (V) sets, so no cross-lane shuffle of KV data is needed.
-// * S^T = K Q^T and O^T += V^T P^T, with the GQA heads in the MFMA N=16
-//   columns (heads >= G are zero).  Softmax reductions are two cross-row
-//   lane exchanges per page; P goes through 2 KB of wave-private LDS.
-// * Escape bytes of a slab are expanded once into wave-private LDS; each lane
+// * One work unit = one 256-thread workgroup (4 wavefronts) walking a chunk
+//   of pages of one (sequence, KV head) with an online softmax.  Per page,
+//   wave w decodes slab w (kernel-order threads 64w..64w+63) of the K record
+//   -- tokens 32w..32w+31 -- and then slab w of the V record -- dims
+//   32w..32w+31 --, so a page costs each wave two decode passes.  Three
+//   workgroup barriers per page: variable region staged, page max known, P
+//   tile complete.
+// * Lane l decodes kernel-order thread nt = 32 hh + 4 g + c of its slab, with
+//   c = l >> 4, hh = (l >> 3) & 1, g = l & 7.  With that assignment the
+//   decoded words are directly the A operands of v_mfma_f32_16x16x32_bf16:
+//   MFMA row = l % 16 indexes the token (K) or dim (V) and the four 16-lane
+//   groups (= c) hold disjoint dim (K) or token (V) sets, so KV data never
+//   moves between lanes.
+// * S^T = K Q^T and O^T += V^T P^T with the group's query heads in the MFMA
+//   N = 16 columns (heads >= G are zero).  Q and P pass through LDS fragment
+//   tiles; each wave keeps O for its 32 dims.
+// * Escape bytes of a slab are expanded into wave-private LDS; each lane
 //   finds its escapes with a kernel-order prefix scan across the wave.
+// * Split-KV partials are merged in the same kernel: the last workgroup to
+//   finish a (sequence, head) merges all its chunks.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -35,9 +39,8 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;  // independent wavefronts per workgroup
+constexpr int kWaves = 4;  // wavefronts per workgroup = slabs per record
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
-constexpr int kWaveLds = kEscLds + kVarCap + 2 * kTileBytes;  // escapes, variable region, P, Q
 constexpr int kPlanThreads = 256;
 
 struct AttnParams {
@@ -51,9 +54,12 @@ struct AttnParams {
   const int32_t* plan;
   float* opart;
   float* ml;
+  uint16_t* out;
+  int32_t* done;      // [kvh, units] merge-group counters (zero between launches)
   int64_t q_stride;   // BF16 elements between sequences
+  int64_t out_stride;
   int64_t bt_stride;  // entries between block-table rows
-  int kvh, group, units;
+  int kvh, group, units, batch;
   float scale_log2;
 };
 
@@ -82,7 +88,7 @@ __device__ __forceinline__ int block_reduce(int v, int* sh) {
 // pages, ``ppc`` the smallest for which the live rows fit ``budget`` units;
 // plan = [ppc, budget, (seq, first page) x units, (first unit, chunks) x B].
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* seq_lens, int32_t* plan, int batch,
-                                                            int units) {
+                                                            int units, int kvh) {
   __shared__ int sh[kPlanThreads / 64];
   __shared__ int wtot[kPlanThreads / 64];
   const int tid = threadIdx.x;
@@ -143,6 +149,9 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* seq_l
     used += tile;
   }
   for (int u = used + tid; u < units; u += kPlanThreads) plan[2 + 2 * u] = -1;
+  // merge-group counters of the fused merge; the last arrival of a group
+  // resets its counter, so zeroing is needed only here
+  for (int x = tid; x < units * kvh; x += kPlanThreads) plan[2 + 4 * units + x] = 0;
   if (tid == 0) {
     plan[0] = ppc;
     plan[1] = budget;
@@ -154,23 +163,39 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
                                                  0, 0);
 }
 
+// Split-KV partials are handed between workgroups (possibly on different
+// XCDs, each with its own L2) through per-location coherent accesses:
+// agent-scope relaxed atomic stores and loads (sc1: written through to, and
+// read from, the device coherence point).  A writer waits for its stores to
+// be acknowledged (s_waitcnt) before bumping the group counter, and a reader
+// issues its loads only after seeing the counter complete.  This avoids the
+// whole-L2 writeback / invalidate an agent-scope fence costs on a multi-XCD
+// part once per workgroup.
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh4(float* p, float a, float b, float c, float d) {
+  st_coh(p, a);
+  st_coh(p + 1, b);
+  st_coh(p + 2, c);
+  st_coh(p + 3, d);
+}
+// Waits until every store this wave issued is acknowledged.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
 // A operand of MFMA (j, a) from words 2a (w0) and 2a+1 (w1) of a lane's
 // decoded thread: slots (x, f, e) = word 2a + x, dword 2j + f, half e.
 __device__ __forceinline__ uint4 a_frag(const uint4& w0, const uint4& w1, int j) {
   return j == 0 ? make_uint4(w0.x, w0.y, w1.x, w1.y) : make_uint4(w0.z, w0.w, w1.z, w1.w);
 }
 
-// Ends a slab step: nothing is scheduled across it, so exactly one slab of
-// loads is in flight while the previous slab is decoded.
-__device__ __forceinline__ void slab_fence() {
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 // Lane of the natural (kernel-order) thread ``nt`` of a slab.
 __device__ __forceinline__ int lane_of_natural(int nt) { return 16 * (nt & 3) + 8 * (nt >> 5) + ((nt >> 2) & 7); }
 
-// A record as the wave sees it (wave-uniform values).
+// A record as the workgroup sees it (uniform values).
 struct RecRef {
   rsrc_t rs;
   int vlen;  // bytes past the dense part; > kVarCap marks a raw record
@@ -184,32 +209,30 @@ __device__ __forceinline__ RecRef rec_ref(const AttnParams& p, int64_t blk, int 
   return r;
 }
 
-// The first 32 bytes per lane of a coded record's variable region, loaded
-// with the record's first slab.
-struct VarPref {
-  uint4 v0, v1;
+// Prefetched data of one decode pass: this lane's dense words of the wave's
+// slab, and this lane's 8 bytes of the wave's quarter of the variable region.
+struct Pref {
+  SlabBuf b;
+  uint2 var;
 };
 
-template <int SLAB>
-__device__ __forceinline__ void prefetch(const RecRef& r, int nt, int lane, SlabBuf& b, VarPref& vp) {
+__device__ __forceinline__ void prefetch(const RecRef& r, int slab, int nt, int lane, Pref& f) {
   const bool raw = r.vlen > kVarCap;
-  load_slab(r.rs, raw, SLAB, nt, b);
-  if constexpr (SLAB == 0) {
-    // Bytes past the record (a short variable region) read as zero.
-    if (!raw) {
-      vp.v0 = bld16(r.rs, 16 * lane, kDenseBytes);
-      vp.v1 = r.vlen > 1024 ? bld16(r.rs, 16 * lane, kDenseBytes + 1024) : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
+  load_slab(r.rs, raw, slab, nt, f.b);
+  f.var = raw ? make_uint2(0u, 0u) : bld8(r.rs, 8 * lane, kDenseBytes + 512 * slab);
 }
 
-// Decodes this lane's kernel-order thread ``nt`` of slab SLAB of record ``r``
-// from prefetched data and calls pair(a, word 2a, word 2a + 1), a = 0..3.
-// ``var`` is the wave's LDS copy of the record's variable region (written
-// here at slab 0), ``esc`` its escape-byte area.
-template <int SLAB, typename Pair>
-__device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, const VarPref& vp, int nt, int lane,
-                                            const HeadLut& lut, uint8_t* var, uint8_t* esc, Pair&& pair) {
+// Copies the wave's quarter of the record's variable region to LDS.
+__device__ __forceinline__ void stage_var(const RecRef& r, const Pref& f, int slab, int lane, uint8_t* var) {
+  if (r.vlen <= kVarCap) *reinterpret_cast<uint2*>(var + 512 * slab + 8 * lane) = f.var;
+}
+
+// Decodes this lane's kernel-order thread ``nt`` of slab ``slab`` of record
+// ``r`` (variable region already in LDS ``var``) and calls
+// pair(a, word 2a, word 2a + 1) for a = 0..3.
+template <typename Pair>
+__device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int slab, int nt, int lane,
+                                            const HeadLut& lut, const uint8_t* var, uint8_t* esc, Pair&& pair) {
   uint4 prev;
   auto emit = [&](auto st_c, const uint4& wd) {
     constexpr int st = decltype(st_c)::value;
@@ -219,16 +242,11 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, c
       prev = wd;
   };
   if (r.vlen > kVarCap) {
-    raw_words(b, r.rs, SLAB, nt, emit);
+    raw_words(b, r.rs, slab, nt, emit);
     return;
   }
-  if constexpr (SLAB == 0) {
-    *reinterpret_cast<uint4*>(var + 16 * lane) = vp.v0;
-    *reinterpret_cast<uint4*>(var + 1024 + 16 * lane) = vp.v1;
-    wave_lds_sync();
-  }
   auto rd4 = [&](int off) { return *reinterpret_cast<const uint32_t*>(var + off); };
-  const SlabHdr h = slab_header(rd4, SLAB);
+  const SlabHdr h = slab_header(rd4, slab);
   stage_escapes(rd4, h, lut.s, esc, lane);
   // kernel-order exclusive prefix of the escape counts
   const int cnt = thread_escapes(b);
@@ -244,14 +262,112 @@ __device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, in
   return *reinterpret_cast<const uint4*>(tile + (((n & 7) * 4 + a) * 4 + c) * 16);
 }
 
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) attn_kernel(AttnParams p) {
-  extern __shared__ __align__(16) uint8_t lds[];
+struct AttnShared {
+  uint8_t esc[kWaves][kEscLds];
+  uint8_t var[2][kVarCap];  // K, V variable regions of the current page
+  uint8_t pt[kTileBytes];   // P tile
+  uint8_t qt[kTileBytes];   // Q tile
+  float red[kWaves][8];     // per-wave page max / final l per head
+  int last;
+};
+
+// Merges ``count`` (<= 8) split-KV partials of (b, h) -- partial rows
+// ``first_row + k * stride`` (k < count) of opart / ml -- with the
+// online-softmax merge in the log2 domain (the reference's combine,
+// fused_attn_decode.cu:407-425).  ``final``: writes the group's BF16 output
+// rows; else writes the merged partial over item 0.  Whole workgroup:
+// thread t covers row t >> 5, dims 4 (t & 31) .. + 3; every load of the
+// group is issued before any is used.
+__device__ __forceinline__ void merge_group(const AttnParams& p, int b, int h, int64_t first_row, int stride,
+                                            int count, bool final) {
+  const int t = threadIdx.x, g = t >> 5, d = 4 * (t & 31);
+  if (g >= p.group) return;
+  float2 ms[8];
+  float4 o[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < count) {
+      const int64_t r = (first_row + (int64_t)k * stride) * 8 + g;
+      ms[k] = make_float2(ld_coh(p.ml + r * 2), ld_coh(p.ml + r * 2 + 1));
+      const float* op = p.opart + r * kDim + d;
+      o[k] = make_float4(ld_coh(op), ld_coh(op + 1), ld_coh(op + 2), ld_coh(op + 3));
+    }
+  }
+  float gm = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < count) gm = fmaxf(gm, ms[k].x);
+  float l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (gm != -INFINITY) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < count) {
+        const float w = __builtin_amdgcn_exp2f(ms[k].x - gm);
+        l += w * ms[k].y;
+        acc.x += w * o[k].x;
+        acc.y += w * o[k].y;
+        acc.z += w * o[k].z;
+        acc.w += w * o[k].w;
+      }
+    }
+  }
+  if (final) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.x * inv)) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.y * inv)) << 16);
+    const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.z * inv)) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.w * inv)) << 16);
+    *reinterpret_cast<uint2*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + g) * kDim + d) =
+        make_uint2(lo, hi);
+  } else {
+    const int64_t r = first_row * 8 + g;
+    st_coh4(p.opart + r * kDim + d, acc.x, acc.y, acc.z, acc.w);
+    if ((t & 31) == 0) {
+      st_coh(p.ml + r * 2, gm);
+      st_coh(p.ml + r * 2 + 1, l);
+    }
+  }
+}
+
+// Hierarchical merge of (b, h)'s ``chunks`` partials after this workgroup
+// wrote chunk ``s``'s.  Items are merged in groups of 8; the last workgroup
+// to finish a group merges it in place over the group's first item, and the
+// last group of the top level writes the output.  Counters live in
+// p.done[h * units + unit slot] and are left at zero.
+__device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh, int b, int h, int first, int chunks,
+                                             int s) {
+  int n_items = chunks, stride = 1;
+  for (int level = 0;; ++level) {
+    const int item = s / stride;
+    const int gfirst = item & ~7;
+    const int gcount = min(8, n_items - gfirst);
+    const bool final = n_items <= 8;
+    if (gcount > 1) {
+      wait_stores();  // this workgroup's partial is at the coherence point
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int32_t* cnt = p.done + (int64_t)h * p.units + first + gfirst * stride + level;
+        const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gcount - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.last = last;
+      }
+      __syncthreads();
+      if (!sh.last) return;
+    }
+    merge_group(p, b, h, (int64_t)h * p.units + first + (int64_t)gfirst * stride, stride, gcount, final);
+    if (final) return;
+    s = gfirst * stride;
+    stride *= 8;
+    n_items = (n_items + 7) >> 3;
+  }
+}
+
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) attn_kernel(AttnParams p) {
+  __shared__ AttnShared sh;
   const int lane = wave_lane();
-  const int wv = threadIdx.x >> 6;
-  uint8_t* esc = lds + wv * kWaveLds;
-  uint8_t* var = esc + kEscLds;
-  uint8_t* pt = var + kVarCap;
-  uint8_t* qt = pt + kTileBytes;
+  const int w = threadIdx.x >> 6;  // this wave's slab of every record
+  uint8_t* esc = sh.esc[w];
   const int h = blockIdx.y;
   const int c = lane >> 4, hh = (lane >> 3) & 1, g = lane & 7;
   const int nt = 32 * hh + 4 * g + c;
@@ -261,20 +377,18 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const HeadLut klut = load_lut(p.plut, p.slut, h);
   const HeadLut vlut = load_lut(p.plut, p.slut, p.kvh + h);
 
-  for (int unit = blockIdx.x * kWaves + wv; unit < budget; unit += gridDim.x * kWaves) {
+  for (int unit = blockIdx.x; unit < budget; unit += gridDim.x) {
     const int b = uniform(p.plan[2 + 2 * unit]);
     if (b < 0) continue;
     const int p0 = uniform(p.plan[3 + 2 * unit]);
     const int seq = uniform(p.seq_lens[b]);
     const int npages = max(0, min((seq + 127) >> 7, p0 + ppc) - p0);
-    if (npages == 0) continue;
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
 
-    // Q tile: element (n, dim) at tile position (n, a = dim / 32, c, slot);
+    __syncthreads();  // the previous unit is done with every tile
+    // Q tile: lane (c, n < 8) of wave 0 writes its four 16-byte fragments;
     // the dims of slot i = 4x + 2f + e of (a, c) are 32a + 16x + 8f + 2c + e.
-    // Lane (c, n < 8) writes its four 16-byte fragments; heads >= G are zero.
-    wave_lds_sync();
-    if (hh == 0) {
+    if (w == 0 && hh == 0) {
       const bool valid = n < p.group;
       const uint32_t* q = reinterpret_cast<const uint32_t*>(p.q + (int64_t)b * p.q_stride +
                                                             (int64_t)(h * p.group + (valid ? n : 0)) * kDim);
@@ -282,162 +396,118 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       for (int a = 0; a < 4; ++a) {
         const int d = 16 * a + c;
         const uint4 v = valid ? make_uint4(q[d], q[d + 4], q[d + 8], q[d + 12]) : make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(qt + ((n * 4 + a) * 4 + c) * 16) = v;
+        *reinterpret_cast<uint4*>(sh.qt + ((n * 4 + a) * 4 + c) * 16) = v;
       }
     }
-    wave_lds_sync();
     float m_run = -INFINITY, l_run = 0.f;
-    f32x4 o[4][2];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) o[s][0] = o[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 
-    const int64_t blk0 = uniform(bt[0]);
-    RecRef kr = rec_ref(p, blk0, 0, h), vr = rec_ref(p, blk0, 1, h);
-    SlabBuf fa, fb;  // double buffer: even slabs of a page in fa, odd in fb
-    VarPref vp;
-    prefetch<0>(kr, nt, lane, fa, vp);
+    RecRef kr = rec_ref(p, uniform(bt[0]), 0, h), vr = rec_ref(p, uniform(bt[0]), 1, h);
+    Pref fk, fv;
+    prefetch(kr, w, nt, lane, fk);
     for (int i = 0; i < npages; ++i) {
       const bool more = i + 1 < npages;
       const int64_t nblk = more ? (int64_t)uniform(bt[i + 1]) : 0;
-      const RecRef nkr = more ? rec_ref(p, nblk, 0, h) : kr;
-      const RecRef nvr = more ? rec_ref(p, nblk, 1, h) : vr;
       const int tok0 = (p0 + i) * kTokens;
+      // V slab of this page in flight while K is decoded
+      prefetch(vr, w, nt, lane, fv);
+      stage_var(kr, fk, w, lane, sh.var[0]);
+      __syncthreads();  // B1: K variable region staged; the previous page's V pass is done everywhere
+      stage_var(vr, fv, w, lane, sh.var[1]);
 
-      // ---- S^T = K Q^T: s[slab][j] rows = tokens, column = head n ----
-      f32x4 s[4][2];
-      static_for<0, 4>([&](auto sl_c) {
-        constexpr int sl = decltype(sl_c)::value;
-        slab_fence();
-        SlabBuf& cur = (sl & 1) ? fb : fa;
-        SlabBuf& nxt = (sl & 1) ? fa : fb;
-        if constexpr (sl < 3)
-          prefetch<sl + 1>(kr, nt, lane, nxt, vp);
-        const VarPref vcur = vp;
-        if constexpr (sl == 3) prefetch<0>(vr, nt, lane, nxt, vp);
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-        decode_slab<sl>(kr, cur, vcur, nt, lane, klut, var, esc, [&](auto a, const uint4& w0, const uint4& w1) {
-          const uint4 qa = tile_frag(qt, n, a, c);
-          acc0 = mfma(a_frag(w0, w1, 0), qa, acc0);
-          acc1 = mfma(a_frag(w0, w1, 1), qa, acc1);
-        });
-        s[sl][0] = acc0;
-        s[sl][1] = acc1;
+      // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      decode_slab(kr, fk.b, w, nt, lane, klut, sh.var[0], esc, [&](auto a, const uint4& w0, const uint4& w1) {
+        const uint4 qa = tile_frag(sh.qt, n, a, c);
+        s0 = mfma(a_frag(w0, w1, 0), qa, s0);
+        s1 = mfma(a_frag(w0, w1, 1), qa, s1);
       });
-      // token of s[sl][j][r] = 32 sl + 16 (c >> 1) + 8 j + 4 (c & 1) + r
+      // token of s_j[r] = 32 w + 16 (c >> 1) + 8 j + 4 (c & 1) + r
+      const int tb = tok0 + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
       float mloc = -INFINITY;
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = tok0 + 32 * sl + 16 * (c >> 1) + 8 * j + 4 * (c & 1) + r;
-            const float v = tok < seq ? s[sl][j][r] * p.scale_log2 : -INFINITY;
-            s[sl][j][r] = v;
-            mloc = fmaxf(mloc, v);
-          }
+      for (int r = 0; r < 4; ++r) {
+        s0[r] = tb + r < seq ? s0[r] * p.scale_log2 : -INFINITY;
+        s1[r] = tb + 8 + r < seq ? s1[r] * p.scale_log2 : -INFINITY;
+        mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
+      }
       mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run, mloc);
+      if (lane < 8) sh.red[w][lane] = mloc;
+      // next page's K slab in flight during the rest of this page
+      if (more) {
+        kr = rec_ref(p, nblk, 0, h);
+        prefetch(kr, w, nt, lane, fk);
+      }
+      __syncthreads();  // B2: page max per wave known
+      float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
+      const float m_new = fmaxf(m_run, mpage);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       m_run = m_new;
-      float psum = 0.f;
+      float e0[4], e1[4], psum = 0.f;
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float e[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            e[r] = __builtin_amdgcn_exp2f(s[sl][j][r] - m_use);
-            psum += e[r];
-          }
-          // P[n][token] -> tile[n][a = sl][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
-          if (hh == 0) {
-            const uint32_t p01 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)e[0]) |
-                                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)e[1]) << 16);
-            const uint32_t p23 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)e[2]) |
-                                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)e[3]) << 16);
-            uint8_t* base = pt + ((n * 4 + sl) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1) + 4 * j;
-            *reinterpret_cast<uint32_t*>(base) = p01;
-            *reinterpret_cast<uint32_t*>(base + 16) = p23;
-          }
-        }
+      for (int r = 0; r < 4; ++r) {
+        e0[r] = __builtin_amdgcn_exp2f(s0[r] - m_use);
+        e1[r] = __builtin_amdgcn_exp2f(s1[r] - m_use);
+        psum += e0[r] + e1[r];
+      }
       l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) o[sl][j] *= alpha;
-      wave_lds_sync();
-      uint4 pf[4];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) pf[a] = tile_frag(pt, n, a, c);
+      o0 *= alpha;
+      o1 *= alpha;
+      // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
+      if (hh == 0) {
+        uint8_t* base = sh.pt + ((n * 4 + w) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1);
+        auto pk = [](float x, float y) {
+          return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
+        };
+        *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e0[1]);
+        *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e0[3]);
+        *reinterpret_cast<uint32_t*>(base + 4) = pk(e1[0], e1[1]);
+        *reinterpret_cast<uint32_t*>(base + 20) = pk(e1[2], e1[3]);
+      }
+      __syncthreads();  // B3: P tile and V variable region complete
 
-      // ---- O^T += V^T P^T: o[slab][j] rows = dims, column = head n ----
-      static_for<0, 4>([&](auto sl_c) {
-        constexpr int sl = decltype(sl_c)::value;
-        slab_fence();
-        SlabBuf& cur = (sl & 1) ? fb : fa;
-        SlabBuf& nxt = (sl & 1) ? fa : fb;
-        if constexpr (sl < 3)
-          prefetch<sl + 1>(vr, nt, lane, nxt, vp);
-        const VarPref vcur = vp;
-        if constexpr (sl == 3) {
-          if (more) prefetch<0>(nkr, nt, lane, nxt, vp);
-        }
-        decode_slab<sl>(vr, cur, vcur, nt, lane, vlut, var, esc, [&](auto a, const uint4& w0, const uint4& w1) {
-          o[sl][0] = mfma(a_frag(w0, w1, 0), pf[a], o[sl][0]);
-          o[sl][1] = mfma(a_frag(w0, w1, 1), pf[a], o[sl][1]);
-        });
+      // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
+      decode_slab(vr, fv.b, w, nt, lane, vlut, sh.var[1], esc, [&](auto a, const uint4& w0, const uint4& w1) {
+        const uint4 pa = tile_frag(sh.pt, n, a, c);
+        o0 = mfma(a_frag(w0, w1, 0), pa, o0);
+        o1 = mfma(a_frag(w0, w1, 1), pa, o1);
       });
-      wave_lds_sync();  // P is rewritten next page
-      kr = nkr;
-      vr = nvr;
+      if (more) vr = rec_ref(p, nblk, 1, h);
     }
 
-    // ---- partial results of this unit ----
+    // ---- this unit's partial: O of the wave's 32 dims, m, and l summed over waves ----
     float l_tot = l_run;
     l_tot += __shfl_xor(l_tot, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
+    __syncthreads();  // everyone is past B2's reads of red
+    if (lane < 8) sh.red[w][lane] = l_tot;
+    const int64_t row = ((int64_t)h * p.units + unit) * 8 + n;
     if (hh == 0) {
-      const int64_t row = ((int64_t)h * p.units + unit) * 8 + n;
-      float* orow = p.opart + row * kDim;
-#pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int d = 32 * sl + 16 * (c >> 1) + 8 * j + 4 * (c & 1);
-          *reinterpret_cast<float4*>(orow + d) = make_float4(o[sl][j][0], o[sl][j][1], o[sl][j][2], o[sl][j][3]);
-        }
-      if (c == 0) {
-        p.ml[row * 2] = m_run;
-        p.ml[row * 2 + 1] = l_tot;
-      }
+      float* orow = p.opart + row * kDim + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
+      st_coh4(orow, o0[0], o0[1], o0[2], o0[3]);
+      st_coh4(orow + 8, o1[0], o1[1], o1[2], o1[3]);
+    }
+    __syncthreads();
+    if (w == 0 && lane < 8) {
+      st_coh(p.ml + row * 2, m_run);
+      st_coh(p.ml + row * 2 + 1, sh.red[0][lane] + sh.red[1][lane] + sh.red[2][lane] + sh.red[3][lane]);
+    }
+    // ---- merge with the other chunks of (b, h) ----
+    const int first = uniform(p.plan[2 + 2 * p.units + 2 * b]);
+    const int chunks = uniform(p.plan[3 + 2 * p.units + 2 * b]);
+    merge_chunks(p, sh, b, h, first, chunks, unit - first);
+  }
+  // rows with no context produce zeros (workgroup 0 of each head)
+  if (blockIdx.x == 0) {
+    for (int b = w; b < p.batch; b += kWaves) {
+      if (p.plan[3 + 2 * p.units + 2 * b] != 0) continue;
+      uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)h * p.group * kDim);
+      for (int x = lane; x < p.group * kDim / 2; x += 64) orow[x] = 0u;
     }
   }
-}
-
-// Merges each sequence's chunk partials; rows with no context are zero.
-__global__ void __launch_bounds__(128) combine_kernel(const float* opart, const float* ml, const int32_t* plan,
-                                                     uint16_t* out, int64_t out_stride, int units, int group) {
-  const int b = blockIdx.x, qh = blockIdx.y, d = threadIdx.x;
-  const int h = qh / group, g = qh % group;
-  const int first = plan[2 + 2 * units + 2 * b], chunks = plan[3 + 2 * units + 2 * b];
-  const int64_t base = (int64_t)h * units + first;
-  float gm = -INFINITY;
-  for (int s = 0; s < chunks; ++s) gm = fmaxf(gm, ml[((base + s) * 8 + g) * 2]);
-  float den = 0.f, acc = 0.f;
-  if (gm != -INFINITY) {
-    for (int s = 0; s < chunks; ++s) {
-      const int64_t r = (base + s) * 8 + g;
-      const float w = __builtin_amdgcn_exp2f(ml[r * 2] - gm);
-      den += w * ml[r * 2 + 1];
-      acc += w * opart[r * kDim + d];
-    }
-  }
-  const float v = den > 0.f ? acc / den : 0.f;
-  out[(int64_t)b * out_stride + (int64_t)qh * kDim + d] = __builtin_bit_cast(uint16_t, (__bf16)v);
 }
 
 }  // namespace
@@ -456,10 +526,12 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   if (batch == 0) return 0;
   FP_CHECK(units >= batch, "decode needs at least one unit per sequence");
   FP_CHECK(q_stride % 2 == 0 && q_stride >= kv_heads * group * kDim, "q must be [B, H, 128] with contiguous heads");
-  FP_CHECK(out_stride >= kv_heads * group * kDim, "out must be [B, H, 128] with contiguous heads");
+  FP_CHECK(out_stride % 2 == 0 && out_stride >= kv_heads * group * kDim && reinterpret_cast<uintptr_t>(out) % 4 == 0,
+           "out must be [B, H, 128] with contiguous heads");
   FP_CHECK(opart_elems >= kv_heads * units * 8 * kDim && ml_elems >= kv_heads * units * 16,
            "decode workspace too small");
-  FP_CHECK(plan_elems >= 2 + 4 * units, "decode plan must be int32 with 2 + 4 * units elements");
+  FP_CHECK(plan_elems >= 2 + 4 * units + units * kv_heads,
+           "decode plan must be int32 with 2 + 4 * units + units * kv_heads elements");
   FP_CHECK(units < (1 << 24) && batch < (1 << 24), "batch too large");
   AttnParams p;
   p.q = static_cast<const uint16_t*>(q);
@@ -477,17 +549,17 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.kvh = (int)kv_heads;
   p.group = (int)group;
   p.units = (int)units;
+  p.batch = (int)batch;
+  p.out = static_cast<uint16_t*>(out);
+  p.out_stride = out_stride;
+  p.done = plan + 2 + 4 * units;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   if (replan) {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, plan, (int)batch, (int)units);
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, plan, (int)batch, (int)units,
+                       (int)kv_heads);
     FP_LAUNCH_CHECK();
   }
-  const int grid_x = (int)((units + kWaves - 1) / kWaves);
-  const size_t lds = (size_t)kWaves * kWaveLds;
-  hipLaunchKernelGGL(attn_kernel, dim3(grid_x, (unsigned)kv_heads), dim3(64 * kWaves), lds, stream, p);
-  FP_LAUNCH_CHECK();
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)batch, (unsigned)(kv_heads * group)), dim3(kDim), 0, stream,
-                     opart, ml, plan, static_cast<uint16_t*>(out), out_stride, (int)units, (int)group);
+  hipLaunchKernelGGL(attn_kernel, dim3((unsigned)units, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);
   FP_LAUNCH_CHECK();
   return 0;
 }

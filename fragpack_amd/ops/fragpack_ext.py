@@ -21,7 +21,10 @@ from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent.parent / "_lib" / "libfragpack_hip.so"
+import os
+
+# FRAGPACK_LIB overrides the library path (e.g. to compare builds).
+LIB_PATH = Path(os.environ.get("FRAGPACK_LIB", Path(__file__).resolve().parent.parent / "_lib" / "libfragpack_hip.so"))
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -136,7 +139,7 @@ class Extension:
         _check(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table rows must be contiguous")
         _check(seq_lens.dtype == torch.int32, "seq_lens must be int32")
         _check(rec_addr.dtype == torch.int64 and rec_len.dtype == torch.int32, "record tables must be int64 / int32")
-        _check(plan.dtype == torch.int32, "decode plan must be int32 with 2 + 4 * units elements")
+        _check(plan.dtype == torch.int32, "decode plan must be int32 with 2 + 4 * units + units * kv_heads elements")
         _check(opart.dtype == torch.float32 and ml.dtype == torch.float32, "decode workspace must be float32")
         B = q.size(0)
         kvh = q.size(1) // group

@@ -6,8 +6,9 @@ fragpack/ops/fused_attn_decode.cu.
 
 One work unit handles a chunk of pages of one (sequence, KV head) pair for
 all query heads of the group, with an online softmax; a small combine kernel
-merges each sequence's chunks.  On gfx950 a unit is one 64-lane wavefront:
-it decodes each record in four passes straight into MFMA operands
+merges each sequence's chunks (here fused into the same kernel: the last
+finished chunk of a (sequence, head) merges them).  On gfx950 a unit is one 256-thread workgroup:
+its four wavefronts decode the four slabs of each record in parallel, straight into MFMA operands
 (``S^T = K Q^T`` and ``O^T += V^T P^T`` with v_mfma_f32_16x16x32_bf16, the
 group's query heads on the N side), so units never synchronise with each
 other.  A one-workgroup planner picks the chunk size on device once per step
@@ -31,9 +32,9 @@ from fragpack_amd.ops.fragpack_ext import extension
 logger = init_logger(__name__)
 
 GQA = 8
-# Work units per compute unit per KV head budget: a unit is one wavefront,
-# and the decode kernel runs 8 wavefronts per CU (2 per SIMD).
-WAVES_PER_CU = 8
+# Split capacity per compute unit: a unit is one 256-thread workgroup and
+# the decode kernel keeps 3 of them resident per CU (3 waves per SIMD).
+UNITS_PER_CU = 3
 
 
 @dataclass(frozen=True)
@@ -58,7 +59,7 @@ def decode_units(batch: int, kv_heads: int, num_sms: int) -> int:
 
     One unit per sequence plus one wave of split capacity minus one, as in
     the reference (fused_attn_decode.py:58-85); a "wave" here is the
-    wavefronts the device runs at once per KV head: ``WAVES_PER_CU`` per
+    workgroups the device runs at once per KV head: ``UNITS_PER_CU`` per
     compute unit.  Depends only on the (padded) batch size, so the launch
     shape is fixed under graph capture.
 
@@ -70,14 +71,19 @@ def decode_units(batch: int, kv_heads: int, num_sms: int) -> int:
     Returns:
         Unit count, at least ``batch``.
     """
-    wave = max(1, (WAVES_PER_CU * num_sms) // max(1, kv_heads))
+    wave = max(1, (UNITS_PER_CU * num_sms) // max(1, kv_heads))
     return batch + wave - 1
 
 
 def workspace_elems(kv_heads: int, units: int) -> tuple[int, int, int]:
-    """Element counts of the ``(opart, ml, plan)`` workspace (float, float, int32)."""
+    """Element counts of the ``(opart, ml, plan)`` workspace (float, float, int32).
+
+    ``plan`` holds the reference's ``2 + 4 * units`` planner words plus one
+    finished-chunk counter per (sequence, KV head) for the merge fused into
+    the attention kernel (``units >= batch``).
+    """
     rows = kv_heads * units * GQA
-    return rows * 128, rows * 2, 2 + 4 * units
+    return rows * 128, rows * 2, 2 + 4 * units + units * kv_heads
 
 
 def decode_attention(
