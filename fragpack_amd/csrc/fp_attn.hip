@@ -60,8 +60,16 @@ struct AttnParams {
   int64_t out_stride;
   int64_t bt_stride;  // entries between block-table rows
   int kvh, group, units, batch;
+  int ud_off;  // int32 offset of the unit descriptors in plan
   float scale_log2;
 };
+
+// Plan layout (int32): [0] ppc, [1] budget, [2, 2 + 2 units) (sequence, first
+// page) per unit (sequence -1: idle), [2 + 2 units, 2 + 4 units) (first
+// unit, chunks) per sequence -- the reference's layout --, then at
+// ud_offset(units) 8 ints per unit (sequence, first page, pages, context,
+// first unit, chunks, 0, 0), then units * kvh merge counters.
+__host__ __device__ __forceinline__ int ud_offset(int units) { return (2 + 4 * units + 7) & ~7; }
 
 __device__ __forceinline__ int pages_of(const int32_t* seq_lens, int b) { return (seq_lens[b] + 127) >> 7; }
 
@@ -141,17 +149,28 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* seq_l
     if (b < batch) {
       seq_plan[2 * b] = first;
       seq_plan[2 * b + 1] = c;
+      const int seq = seq_lens[b], pages = pages_of(seq_lens, b);
       for (int s = 0; s < c; ++s) {
         plan[2 + 2 * (first + s)] = b;
         plan[3 + 2 * (first + s)] = s * ppc;
+        int32_t* ud = plan + ud_offset(units) + 8 * (first + s);
+        ud[0] = b;
+        ud[1] = s * ppc;
+        ud[2] = min(pages, (s + 1) * ppc) - s * ppc;
+        ud[3] = seq;
+        ud[4] = first;
+        ud[5] = c;
       }
     }
     used += tile;
   }
-  for (int u = used + tid; u < units; u += kPlanThreads) plan[2 + 2 * u] = -1;
+  for (int u = used + tid; u < units; u += kPlanThreads) {
+    plan[2 + 2 * u] = -1;
+    plan[ud_offset(units) + 8 * u] = -1;
+  }
   // merge-group counters of the fused merge; the last arrival of a group
   // resets its counter, so zeroing is needed only here
-  for (int x = tid; x < units * kvh; x += kPlanThreads) plan[2 + 4 * units + x] = 0;
+  for (int x = tid; x < units * kvh; x += kPlanThreads) plan[ud_offset(units) + 8 * units + x] = 0;
   if (tid == 0) {
     plan[0] = ppc;
     plan[1] = budget;
@@ -201,38 +220,116 @@ struct RecRef {
   int vlen;  // bytes past the dense part; > kVarCap marks a raw record
 };
 
-__device__ __forceinline__ RecRef rec_ref(const AttnParams& p, int64_t blk, int kv, int h) {
-  const int64_t idx = (blk * 2 + kv) * p.kvh + h;
+__device__ __forceinline__ RecRef make_ref(uint32_t lo, uint32_t hi, int vlen) {
   RecRef r;
-  r.rs = make_rsrc(reinterpret_cast<const uint8_t*>(uniform64(p.rec_addr[idx])), kRawRecord);
-  r.vlen = uniform(p.rec_len[idx]);
+  r.rs = make_rsrc(reinterpret_cast<const uint8_t*>((uint64_t)lo | ((uint64_t)hi << 32)), kRawRecord);
+  r.vlen = vlen;
   return r;
 }
 
-// Prefetched data of one decode pass: this lane's dense words of the wave's
-// slab, and this lane's 8 bytes of the wave's quarter of the variable region.
-struct Pref {
-  SlabBuf b;
-  uint2 var;
+// Record metadata of up to 64 pages of a unit, page i in lane i: K / V
+// record address (lo, hi) and length.
+struct PageMeta {
+  uint32_t klo, khi, vlo, vhi;
+  int klen, vlen;
 };
 
-__device__ __forceinline__ void prefetch(const RecRef& r, int slab, int nt, int lane, Pref& f) {
-  const bool raw = r.vlen > kVarCap;
-  load_slab(r.rs, raw, slab, nt, f.b);
-  f.var = raw ? make_uint2(0u, 0u) : bld8(r.rs, 8 * lane, kDenseBytes + 512 * slab);
+__device__ __forceinline__ PageMeta load_meta(const AttnParams& p, const int32_t* bt, int base, int npages, int h,
+                                              int lane) {
+  PageMeta m{0u, 0u, 0u, 0u, kRawVarLen, kRawVarLen};
+  if (base + lane < npages) {
+    const int64_t kidx = ((int64_t)bt[base + lane] * 2) * p.kvh + h;
+    const uint64_t ka = (uint64_t)p.rec_addr[kidx], va = (uint64_t)p.rec_addr[kidx + p.kvh];
+    m.klo = (uint32_t)ka;
+    m.khi = (uint32_t)(ka >> 32);
+    m.vlo = (uint32_t)va;
+    m.vhi = (uint32_t)(va >> 32);
+    m.klen = p.rec_len[kidx];
+    m.vlen = p.rec_len[kidx + p.kvh];
+  }
+  return m;
 }
 
-// Copies the wave's quarter of the record's variable region to LDS.
-__device__ __forceinline__ void stage_var(const RecRef& r, const Pref& f, int slab, int lane, uint8_t* var) {
-  if (r.vlen <= kVarCap) *reinterpret_cast<uint2*>(var + 512 * slab + 8 * lane) = f.var;
+__device__ __forceinline__ RecRef page_ref(const PageMeta& m, int i, int kv) {
+  const int l = i & 63;
+  return kv == 0 ? make_ref(__builtin_amdgcn_readlane(m.klo, l), __builtin_amdgcn_readlane(m.khi, l),
+                            __builtin_amdgcn_readlane(m.klen, l))
+                 : make_ref(__builtin_amdgcn_readlane(m.vlo, l), __builtin_amdgcn_readlane(m.vhi, l),
+                            __builtin_amdgcn_readlane(m.vlen, l));
 }
 
-// Decodes this lane's kernel-order thread ``nt`` of slab ``slab`` of record
-// ``r`` (variable region already in LDS ``var``) and calls
+// Dense words of the wave's slab ``slab`` of record ``r``.
+__device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt, SlabBuf& b) {
+  load_slab(r.rs, r.vlen > kVarCap, slab, nt, b);
+}
+
+// This lane's 8 bytes (at 512 w + 8 lane) of the record's variable region.
+__device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane) {
+  return r.vlen > kVarCap ? make_uint2(0u, 0u) : bld8(r.rs, 8 * lane, kDenseBytes + 512 * w);
+}
+
+// Per-record escape staging, done by all four waves from their prefetched
+// quarters of the variable region: (1) nibble bytes -> table bytes into the
+// record's LDS escape area (byte k = escape ordinal k) and the header into
+// LDS; then, after a barrier, (2) raw-list entries patch their escapes.
+__device__ __forceinline__ void expand_var(const RecRef& r, uint2 v, int w, int lane, const uint32_t (&sl)[4],
+                                           uint8_t* esc, uint32_t* hdr) {
+  if (r.vlen > kVarCap) return;
+  const int o = 512 * w + 8 * lane;
+  if (o >= kHeaderBytes) {
+    const uint2 e0 = expand_nibbles(v.x, sl), e1 = expand_nibbles(v.y, sl);
+    *reinterpret_cast<uint4*>(esc + 2 * (o - kHeaderBytes)) = make_uint4(e0.x, e0.y, e1.x, e1.y);
+  } else {
+    hdr[o >> 2] = v.x;
+    hdr[(o >> 2) + 1] = v.y;
+  }
+}
+
+__device__ __forceinline__ void patch_raw(const RecRef& r, uint2 v, int w, int lane, uint8_t* esc,
+                                          const uint32_t* hdr) {
+  if (r.vlen > kVarCap) return;
+  const int n_raw = (int)hdr[1], raw_offset = (int)hdr[2];
+  const int o = 512 * w + 8 * lane;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int off = o + 4 * q;
+    if (off >= raw_offset && ((off - raw_offset) >> 2) < n_raw) {
+      const uint32_t e = q ? v.y : v.x;
+      const int x = (int)(e & 0xFFFFu);
+      if (x < kEscLds) esc[x] = (uint8_t)(e >> 16);
+    }
+  }
+}
+
+// Lanes (in MFMA lane order) whose kernel-order thread precedes this lane's:
+// natural index 32 hh + 4 g + c, lane 16 c + 8 hh + g.
+__device__ __forceinline__ uint64_t natural_below(int c, int hh, int g) {
+  uint64_t m = 0;
+  if (hh) m |= 0x00FF00FF00FF00FFull;
+  m |= (uint64_t)(((1u << g) - 1u) << (8 * hh)) * 0x0001000100010001ull;
+  for (int cc = 0; cc < c; ++cc) m |= 1ull << (16 * cc + 8 * hh + g);
+  return m;
+}
+
+// Exclusive prefix (in kernel order) of ``cnt`` (0..64) over the wave, from
+// bit-sliced ballots: sum_b 2^b popcount(ballot_b & below).
+__device__ __forceinline__ int natural_prefix(int cnt, uint64_t below) {
+  int x = 0;
+#pragma unroll
+  for (int b = 0; b < 7; ++b) {
+    const uint64_t m = __ballot((cnt >> b) & 1);
+    if (m) x += __builtin_popcountll(m & below) << b;
+  }
+  return x;
+}
+
+// Decodes this lane's kernel-order thread ``nt`` of the wave's slab ``w`` of
+// record ``r`` (escapes staged in ``esc``, header in ``hdr``) and calls
 // pair(a, word 2a, word 2a + 1) for a = 0..3.
 template <typename Pair>
-__device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int slab, int nt, int lane,
-                                            const HeadLut& lut, const uint8_t* var, uint8_t* esc, Pair&& pair) {
+__device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int w, int nt, uint64_t below,
+                                            const HeadLut& lut, const uint8_t* esc, const uint32_t* hdr,
+                                            Pair&& pair) {
   uint4 prev;
   auto emit = [&](auto st_c, const uint4& wd) {
     constexpr int st = decltype(st_c)::value;
@@ -242,18 +339,12 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
       prev = wd;
   };
   if (r.vlen > kVarCap) {
-    raw_words(b, r.rs, slab, nt, emit);
+    raw_words(b, r.rs, w, nt, emit);
     return;
   }
-  auto rd4 = [&](int off) { return *reinterpret_cast<const uint32_t*>(var + off); };
-  const SlabHdr h = slab_header(rd4, slab);
-  stage_escapes(rd4, h, lut.s, esc, lane);
-  // kernel-order exclusive prefix of the escape counts
-  const int cnt = thread_escapes(b);
-  const int v_nat = __shfl(cnt, lane_of_natural(lane), 64);
-  const int incl = wave_incl_scan(v_nat);
-  const int excl = __shfl(incl - v_nat, nt, 64);
-  decode_words(b, esc, (h.e0 & 7) + excl, lut.p0, lut.p1, emit);
+  const int e0 = (int)(hdr[4 + w] & 0xFFFFu);  // esc_prefix[2 w]
+  const int excl = natural_prefix(thread_escapes(b), below);
+  decode_words(b, esc, e0 + excl, lut.p0, lut.p1, emit);
 }
 
 // Fragment tile [head 8][a 4][c 4] x 16 B: lane (c, n) reads its 8 BF16 of
@@ -262,12 +353,28 @@ __device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, in
   return *reinterpret_cast<const uint4*>(tile + (((n & 7) * 4 + a) * 4 + c) * 16);
 }
 
+// Optional per-workgroup timeline (built only with -DFP_TRACE): slot k of
+// workgroup (x, y) holds s_memrealtime (100 MHz) at trace point k.
+#ifdef FP_TRACE
+constexpr int kTraceSlots = 32;
+__device__ uint64_t fp_trace_buf[4096 * kTraceSlots];
+#define FP_STAMP(k)                                                                                 \
+  do {                                                                                              \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096 && (k) < kTraceSlots)              \
+      fp_trace_buf[blockIdx.x * kTraceSlots + (k)] = __builtin_amdgcn_s_memrealtime();                \
+  } while (0)
+#else
+#define FP_STAMP(k) \
+  do {              \
+  } while (0)
+#endif
+
 struct AttnShared {
-  uint8_t esc[kWaves][kEscLds];
-  uint8_t var[2][kVarCap];  // K, V variable regions of the current page
-  uint8_t pt[kTileBytes];   // P tile
-  uint8_t qt[kTileBytes];   // Q tile
-  float red[kWaves][8];     // per-wave page max / final l per head
+  uint8_t esc[2][2][kEscLds];  // [page parity][K, V] expanded escape bytes
+  uint32_t hdr[2][2][12];      // [page parity][K, V] record headers
+  uint8_t pt[kTileBytes];      // P tile
+  uint8_t qt[kTileBytes];      // Q tile
+  float red[kWaves][8];        // per-wave page max / final l per head
   int last;
 };
 
@@ -337,6 +444,7 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int b, int h, i
 // p.done[h * units + unit slot] and are left at zero.
 __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh, int b, int h, int first, int chunks,
                                              int s) {
+  // chunks >= 2: a single chunk writes its output directly
   int n_items = chunks, stride = 1;
   for (int level = 0;; ++level) {
     const int item = s / stride;
@@ -354,8 +462,9 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
       }
       __syncthreads();
       if (!sh.last) return;
+      merge_group(p, b, h, (int64_t)h * p.units + first + (int64_t)gfirst * stride, stride, gcount, final);
     }
-    merge_group(p, b, h, (int64_t)h * p.units + first + (int64_t)gfirst * stride, stride, gcount, final);
+    // gcount == 1 (never final): the item moves up a level in place
     if (final) return;
     s = gfirst * stride;
     stride *= 8;
@@ -367,25 +476,28 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   __shared__ AttnShared sh;
   const int lane = wave_lane();
   const int w = threadIdx.x >> 6;  // this wave's slab of every record
-  uint8_t* esc = sh.esc[w];
   const int h = blockIdx.y;
   const int c = lane >> 4, hh = (lane >> 3) & 1, g = lane & 7;
   const int nt = 32 * hh + 4 * g + c;
+  const uint64_t below = natural_below(c, hh, g);
   const int n = lane & 15;  // MFMA column = query head within the group
   const int budget = uniform(p.plan[1]);
-  const int ppc = uniform(p.plan[0]);
   const HeadLut klut = load_lut(p.plut, p.slut, h);
   const HeadLut vlut = load_lut(p.plut, p.slut, p.kvh + h);
 
+  FP_STAMP(0);
   for (int unit = blockIdx.x; unit < budget; unit += gridDim.x) {
-    const int b = uniform(p.plan[2 + 2 * unit]);
+    // unit descriptor: b, first page, pages, context, first unit of b, chunks of b
+    const int32_t* ud = p.plan + p.ud_off + 8 * unit;
+    const int b = uniform(ud[0]);
     if (b < 0) continue;
-    const int p0 = uniform(p.plan[3 + 2 * unit]);
-    const int seq = uniform(p.seq_lens[b]);
-    const int npages = max(0, min((seq + 127) >> 7, p0 + ppc) - p0);
+    const int p0 = uniform(ud[1]), npages = uniform(ud[2]), seq = uniform(ud[3]);
+    const int first = uniform(ud[4]), chunks = uniform(ud[5]);
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
+    PageMeta meta = load_meta(p, bt, 0, npages, h, lane);
 
     __syncthreads();  // the previous unit is done with every tile
+    FP_STAMP(1);
     // Q tile: lane (c, n < 8) of wave 0 writes its four 16-byte fragments;
     // the dims of slot i = 4x + 2f + e of (a, c) are 32a + 16x + 8f + 2c + e.
     if (w == 0 && hh == 0) {
@@ -402,26 +514,44 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 
-    RecRef kr = rec_ref(p, uniform(bt[0]), 0, h), vr = rec_ref(p, uniform(bt[0]), 1, h);
-    Pref fk, fv;
-    prefetch(kr, w, nt, lane, fk);
+    // page 0: dense K slab and both variable regions, staged before the loop
+    RecRef kr = page_ref(meta, 0, 0), vr = page_ref(meta, 0, 1);
+    FP_STAMP(2);
+    SlabBuf fk, fv;
+    prefetch_dense(kr, w, nt, fk);
+    uint2 vk = prefetch_var(kr, w, lane), vv = prefetch_var(vr, w, lane);
+    expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
+    expand_var(vr, vv, w, lane, vlut.s, sh.esc[0][1], sh.hdr[0][1]);
+    __syncthreads();
+    patch_raw(kr, vk, w, lane, sh.esc[0][0], sh.hdr[0][0]);
+    patch_raw(vr, vv, w, lane, sh.esc[0][1], sh.hdr[0][1]);
+
     for (int i = 0; i < npages; ++i) {
+      const int par = i & 1;
       const bool more = i + 1 < npages;
-      const int64_t nblk = more ? (int64_t)uniform(bt[i + 1]) : 0;
       const int tok0 = (p0 + i) * kTokens;
-      // V slab of this page in flight while K is decoded
-      prefetch(vr, w, nt, lane, fv);
-      stage_var(kr, fk, w, lane, sh.var[0]);
-      __syncthreads();  // B1: K variable region staged; the previous page's V pass is done everywhere
-      stage_var(vr, fv, w, lane, sh.var[1]);
+      if (more && ((i + 1) & 63) == 0) meta = load_meta(p, bt, i + 1, npages, h, lane);
+      // V slab of this page in flight while K is decoded; the next page's
+      // variable regions in flight for the whole page
+      prefetch_dense(vr, w, nt, fv);
+      RecRef nkr = kr, nvr = vr;
+      if (more) {
+        nkr = page_ref(meta, i + 1, 0);
+        nvr = page_ref(meta, i + 1, 1);
+        vk = prefetch_var(nkr, w, lane);
+        vv = prefetch_var(nvr, w, lane);
+      }
+      __syncthreads();  // B1: this page's escapes patched; the previous page's V pass done everywhere
+      FP_STAMP(3 + 5 * min(i, 4));
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      decode_slab(kr, fk.b, w, nt, lane, klut, sh.var[0], esc, [&](auto a, const uint4& w0, const uint4& w1) {
-        const uint4 qa = tile_frag(sh.qt, n, a, c);
-        s0 = mfma(a_frag(w0, w1, 0), qa, s0);
-        s1 = mfma(a_frag(w0, w1, 1), qa, s1);
-      });
+      decode_slab(kr, fk, w, nt, below, klut, sh.esc[par][0], sh.hdr[par][0],
+                  [&](auto a, const uint4& w0, const uint4& w1) {
+                    const uint4 qa = tile_frag(sh.qt, n, a, c);
+                    s0 = mfma(a_frag(w0, w1, 0), qa, s0);
+                    s1 = mfma(a_frag(w0, w1, 1), qa, s1);
+                  });
       // token of s_j[r] = 32 w + 16 (c >> 1) + 8 j + 4 (c & 1) + r
       const int tb = tok0 + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
       float mloc = -INFINITY;
@@ -434,12 +564,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
       if (lane < 8) sh.red[w][lane] = mloc;
-      // next page's K slab in flight during the rest of this page
+      FP_STAMP(4 + 5 * min(i, 4));
       if (more) {
-        kr = rec_ref(p, nblk, 0, h);
-        prefetch(kr, w, nt, lane, fk);
+        prefetch_dense(nkr, w, nt, fk);
+        expand_var(nkr, vk, w, lane, klut.s, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
+        expand_var(nvr, vv, w, lane, vlut.s, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
       }
-      __syncthreads();  // B2: page max per wave known
+      __syncthreads();  // B2: page max per wave known; next page's escapes expanded
+      FP_STAMP(5 + 5 * min(i, 4));
       float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
       const float m_new = fmaxf(m_run, mpage);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -467,38 +599,61 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         *reinterpret_cast<uint32_t*>(base + 4) = pk(e1[0], e1[1]);
         *reinterpret_cast<uint32_t*>(base + 20) = pk(e1[2], e1[3]);
       }
-      __syncthreads();  // B3: P tile and V variable region complete
+      if (more) {
+        patch_raw(nkr, vk, w, lane, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
+        patch_raw(nvr, vv, w, lane, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
+      }
+      __syncthreads();  // B3: P tile complete
+      FP_STAMP(6 + 5 * min(i, 4));
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
-      decode_slab(vr, fv.b, w, nt, lane, vlut, sh.var[1], esc, [&](auto a, const uint4& w0, const uint4& w1) {
-        const uint4 pa = tile_frag(sh.pt, n, a, c);
-        o0 = mfma(a_frag(w0, w1, 0), pa, o0);
-        o1 = mfma(a_frag(w0, w1, 1), pa, o1);
-      });
-      if (more) vr = rec_ref(p, nblk, 1, h);
+      decode_slab(vr, fv, w, nt, below, vlut, sh.esc[par][1], sh.hdr[par][1],
+                  [&](auto a, const uint4& w0, const uint4& w1) {
+                    const uint4 pa = tile_frag(sh.pt, n, a, c);
+                    o0 = mfma(a_frag(w0, w1, 0), pa, o0);
+                    o1 = mfma(a_frag(w0, w1, 1), pa, o1);
+                  });
+      kr = nkr;
+      vr = nvr;
+      FP_STAMP(7 + 5 * min(i, 4));
     }
 
-    // ---- this unit's partial: O of the wave's 32 dims, m, and l summed over waves ----
+    // ---- this unit's result: O of the wave's 32 dims, m, and l summed over waves ----
     float l_tot = l_run;
     l_tot += __shfl_xor(l_tot, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
     __syncthreads();  // everyone is past B2's reads of red
     if (lane < 8) sh.red[w][lane] = l_tot;
+    __syncthreads();
+    const float l_all = sh.red[0][n & 7] + sh.red[1][n & 7] + sh.red[2][n & 7] + sh.red[3][n & 7];
+    if (chunks == 1) {
+      // the whole sequence in one unit: normalise and write the output rows
+      if (hh == 0 && n < p.group) {
+        const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
+        auto pk = [](float x, float y) {
+          return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
+        };
+        uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + n) * kDim + 32 * w +
+                         16 * (c >> 1) + 4 * (c & 1);
+        *reinterpret_cast<uint2*>(orow) = make_uint2(pk(o0[0] * inv, o0[1] * inv), pk(o0[2] * inv, o0[3] * inv));
+        *reinterpret_cast<uint2*>(orow + 8) = make_uint2(pk(o1[0] * inv, o1[1] * inv), pk(o1[2] * inv, o1[3] * inv));
+      }
+      continue;
+    }
     const int64_t row = ((int64_t)h * p.units + unit) * 8 + n;
     if (hh == 0) {
       float* orow = p.opart + row * kDim + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
       st_coh4(orow, o0[0], o0[1], o0[2], o0[3]);
       st_coh4(orow + 8, o1[0], o1[1], o1[2], o1[3]);
+      if (w == 0 && c == 0) {
+        st_coh(p.ml + row * 2, m_run);
+        st_coh(p.ml + row * 2 + 1, l_all);
+      }
     }
-    __syncthreads();
-    if (w == 0 && lane < 8) {
-      st_coh(p.ml + row * 2, m_run);
-      st_coh(p.ml + row * 2 + 1, sh.red[0][lane] + sh.red[1][lane] + sh.red[2][lane] + sh.red[3][lane]);
-    }
-    // ---- merge with the other chunks of (b, h) ----
-    const int first = uniform(p.plan[2 + 2 * p.units + 2 * b]);
-    const int chunks = uniform(p.plan[3 + 2 * p.units + 2 * b]);
+    FP_STAMP(28);
     merge_chunks(p, sh, b, h, first, chunks, unit - first);
+    FP_STAMP(29);
   }
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
@@ -515,6 +670,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
 using namespace fp;
 
+#ifdef FP_TRACE
+extern "C" int fp_trace_read(uint64_t* host, int64_t n) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(fp_trace_buf), n * sizeof(uint64_t)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
                                const int64_t* rec_addr, const int32_t* rec_len, const uint32_t* plut,
                                const uint8_t* slut, const int32_t* block_table, int64_t bt_stride,
@@ -530,8 +691,9 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
            "out must be [B, H, 128] with contiguous heads");
   FP_CHECK(opart_elems >= kv_heads * units * 8 * kDim && ml_elems >= kv_heads * units * 16,
            "decode workspace too small");
-  FP_CHECK(plan_elems >= 2 + 4 * units + units * kv_heads,
-           "decode plan must be int32 with 2 + 4 * units + units * kv_heads elements");
+  FP_CHECK(units < (1 << 24) && batch < (1 << 24), "batch too large");
+  FP_CHECK(plan_elems >= ud_offset((int)units) + 8 * units + units * kv_heads,
+           "decode plan workspace too small (see workspace_elems)");
   FP_CHECK(units < (1 << 24) && batch < (1 << 24), "batch too large");
   AttnParams p;
   p.q = static_cast<const uint16_t*>(q);
@@ -552,7 +714,8 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.batch = (int)batch;
   p.out = static_cast<uint16_t*>(out);
   p.out_stride = out_stride;
-  p.done = plan + 2 + 4 * units;
+  p.ud_off = ud_offset((int)units);
+  p.done = plan + p.ud_off + 8 * units;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   if (replan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, plan, (int)batch, (int)units,

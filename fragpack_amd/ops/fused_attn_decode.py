@@ -78,12 +78,12 @@ def decode_units(batch: int, kv_heads: int, num_sms: int) -> int:
 def workspace_elems(kv_heads: int, units: int) -> tuple[int, int, int]:
     """Element counts of the ``(opart, ml, plan)`` workspace (float, float, int32).
 
-    ``plan`` holds the reference's ``2 + 4 * units`` planner words plus one
-    finished-chunk counter per (sequence, KV head) for the merge fused into
-    the attention kernel (``units >= batch``).
+    ``plan`` holds the reference's ``2 + 4 * units`` planner words (padded to
+    8), an 8-int descriptor per unit and ``units * kv_heads`` counters for the
+    merge fused into the attention kernel.
     """
     rows = kv_heads * units * GQA
-    return rows * 128, rows * 2, 2 + 4 * units + units * kv_heads
+    return rows * 128, rows * 2, ((2 + 4 * units + 7) & ~7) + 8 * units + units * kv_heads
 
 
 def decode_attention(
