@@ -292,6 +292,22 @@ def cpu_baseline(torch, res, args) -> dict:
                 f"record decode + fp32 attention), {per * 1e3:.0f} ms each")
 
 
+def profiled_traffic(kernel: str, workload: str) -> dict | None:
+    """HBM bytes per launch of ``kernel`` measured with rocprofv3 PMC passes
+    (FETCH_SIZE, WRITE_SIZE, scaled by a plain copy's counters), read from
+    the committed summary profiles/<kernel>_<workload>.md (lines
+    ``key: value``); None if absent."""
+    path = ROOT / "profiles" / f"{kernel}_{workload}.md"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if ":" in line and line.split(":")[0].strip() in ("traffic_bytes_per_launch", "fetch_bytes", "write_bytes"):
+            k, v = line.split(":", 1)
+            vals[k.strip()] = int(float(v.strip().split()[0]))
+    return vals or None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -308,7 +324,19 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-encode", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy 3x (scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        src = torch.ones(1 << 28, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 4 << 28, "copies": 3}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus N > 1 is not supported (see DESIGN.md, "
                                    "'How the path would shard')"}))
@@ -323,6 +351,9 @@ def main() -> None:
     step_s = res["step_ms"] / 1e3
     kern_s = res["kern_ms"] / 1e3
     achieved = res["algo_bytes"] / kern_s / 1e9
+    default_shape = (args.batch, args.heads, args.group, args.context) == (4, 4, 8, 8192)
+    prof = profiled_traffic("attn_kernel", "config1") if default_shape else None
+    traffic = prof.get("traffic_bytes_per_launch") if prof else None
     line = {
         "metric": "decode-attn effective BF16-KV GB/s (us/step, compressed GB/s, encode GB/s alongside)",
         "value": round(res["eff_bytes"] / step_s / 1e9, 2),
@@ -346,7 +377,7 @@ def main() -> None:
         "max_abs_err": res["max_err"],
         "roofline": {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "us_per_launch": round(res["kern_ms"] * 1e3, 2),
+                     "traffic": traffic, "us_per_launch": round(res["kern_ms"] * 1e3, 2),
                      "algo_bytes_per_launch": res["algo_bytes"]},
         "cpu_baseline": cpu,
     }

@@ -38,6 +38,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;  // wavefronts per workgroup = slabs per record
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
@@ -190,17 +191,25 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
 // issues its loads only after seeing the counter complete.  This avoids the
 // whole-L2 writeback / invalidate an agent-scope fence costs on a multi-XCD
 // part once per workgroup.
-__device__ __forceinline__ void st_coh(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Coherent (sc1) 16- / 8-byte accesses through a buffer resource over a
+// float array of < 2^31 bytes; ``i`` is the float index.
+constexpr int kSc1 = 16;  // cache-policy bit of buffer instructions: sc1
+__device__ __forceinline__ rsrc_t coh_rsrc(const float* base) { return make_rsrc(base, 0x7fffffff); }
+__device__ __forceinline__ void st_coh4(rsrc_t r, int64_t i, float a, float b, float c, float d) {
+  const f32x4 v = {a, b, c, d};
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)(4 * i), 0, kSc1);
 }
-__device__ __forceinline__ float ld_coh(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_coh2(rsrc_t r, int64_t i, float a, float b) {
+  const float2v v = {a, b};
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, (int)(4 * i), 0, kSc1);
 }
-__device__ __forceinline__ void st_coh4(float* p, float a, float b, float c, float d) {
-  st_coh(p, a);
-  st_coh(p + 1, b);
-  st_coh(p + 2, c);
-  st_coh(p + 3, d);
+__device__ __forceinline__ float4 ld_coh4(rsrc_t r, int64_t i) {
+  const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(4 * i), 0, kSc1));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float2 ld_coh2(rsrc_t r, int64_t i) {
+  const float2v v = __builtin_bit_cast(float2v, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(4 * i), 0, kSc1));
+  return make_float2(v[0], v[1]);
 }
 // Waits until every store this wave issued is acknowledged.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
@@ -389,15 +398,15 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int b, int h, i
                                             int count, bool final) {
   const int t = threadIdx.x, g = t >> 5, d = 4 * (t & 31);
   if (g >= p.group) return;
+  const rsrc_t ro = coh_rsrc(p.opart), rm = coh_rsrc(p.ml);
   float2 ms[8];
   float4 o[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     if (k < count) {
       const int64_t r = (first_row + (int64_t)k * stride) * 8 + g;
-      ms[k] = make_float2(ld_coh(p.ml + r * 2), ld_coh(p.ml + r * 2 + 1));
-      const float* op = p.opart + r * kDim + d;
-      o[k] = make_float4(ld_coh(op), ld_coh(op + 1), ld_coh(op + 2), ld_coh(op + 3));
+      ms[k] = ld_coh2(rm, r * 2);
+      o[k] = ld_coh4(ro, r * kDim + d);
     }
   }
   float gm = -INFINITY;
@@ -429,11 +438,8 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int b, int h, i
         make_uint2(lo, hi);
   } else {
     const int64_t r = first_row * 8 + g;
-    st_coh4(p.opart + r * kDim + d, acc.x, acc.y, acc.z, acc.w);
-    if ((t & 31) == 0) {
-      st_coh(p.ml + r * 2, gm);
-      st_coh(p.ml + r * 2 + 1, l);
-    }
+    st_coh4(ro, r * kDim + d, acc.x, acc.y, acc.z, acc.w);
+    if ((t & 31) == 0) st_coh2(rm, r * 2, gm, l);
   }
 }
 
@@ -643,13 +649,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     const int64_t row = ((int64_t)h * p.units + unit) * 8 + n;
     if (hh == 0) {
-      float* orow = p.opart + row * kDim + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
-      st_coh4(orow, o0[0], o0[1], o0[2], o0[3]);
-      st_coh4(orow + 8, o1[0], o1[1], o1[2], o1[3]);
-      if (w == 0 && c == 0) {
-        st_coh(p.ml + row * 2, m_run);
-        st_coh(p.ml + row * 2 + 1, l_all);
-      }
+      const rsrc_t ro = coh_rsrc(p.opart);
+      const int64_t i0 = row * kDim + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
+      st_coh4(ro, i0, o0[0], o0[1], o0[2], o0[3]);
+      st_coh4(ro, i0 + 8, o1[0], o1[1], o1[2], o1[3]);
+      if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run, l_all);
     }
     FP_STAMP(28);
     merge_chunks(p, sh, b, h, first, chunks, unit - first);
@@ -692,6 +696,7 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   FP_CHECK(opart_elems >= kv_heads * units * 8 * kDim && ml_elems >= kv_heads * units * 16,
            "decode workspace too small");
   FP_CHECK(units < (1 << 24) && batch < (1 << 24), "batch too large");
+  FP_CHECK(kv_heads * units * 8 * kDim * 4 < (1LL << 31), "decode workspace must stay below 2 GiB");
   FP_CHECK(plan_elems >= ud_offset((int)units) + 8 * units + units * kv_heads,
            "decode plan workspace too small (see workspace_elems)");
   FP_CHECK(units < (1 << 24) && batch < (1 << 24), "batch too large");
