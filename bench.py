@@ -173,25 +173,26 @@ def decode_bench(torch, args) -> dict:
     algo_bytes = rec_bytes + meta_bytes + qo_bytes
     eff_bytes = 2 * B * pages * T * H * D * 2
 
+    stream = torch.cuda.current_stream()
+
+    def timed(fn) -> float:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step(True)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    step_ms = e0.elapsed_time(e1) / args.steps
+    # one step = the plan kernel + the attention kernel, launched eagerly
+    # (two host launches; a HIP graph replay of the same step measured slower
+    # on this stack: ~8 us between replays)
+    step_ms = timed(step)
     # the attention kernel alone (replan=False launches only attn_kernel)
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(stream)
-    for _ in range(args.steps):
-        step(False)
-    k1.record(stream)
-    torch.cuda.synchronize()
-    kern_ms = k0.elapsed_time(k1) / args.steps
+    kern_ms = timed(lambda: step(False))
     comp_ratio = rec_bytes / (2 * used.size * H * 32768)
     log(f"step {step_ms * 1e3:.1f} us, attn kernel {kern_ms * 1e3:.1f} us, "
         f"compressed {rec_bytes / 1e6:.1f} MB ({comp_ratio:.3f} of raw), effective BF16 {eff_bytes / 1e6:.1f} MB")

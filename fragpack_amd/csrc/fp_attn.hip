@@ -42,7 +42,6 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;  // wavefronts per workgroup = slabs per record
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
-constexpr int kPlanThreads = 256;
 
 struct AttnParams {
   const uint16_t* q;
@@ -69,113 +68,178 @@ struct AttnParams {
 // page) per unit (sequence -1: idle), [2 + 2 units, 2 + 4 units) (first
 // unit, chunks) per sequence -- the reference's layout --, then at
 // ud_offset(units) 8 ints per unit (sequence, first page, pages, context,
-// first unit, chunks, 0, 0), then units * kvh merge counters.
+// first unit, chunks, block of page 0, block of page 1), then units * kvh
+// merge counters.
 __host__ __device__ __forceinline__ int ud_offset(int units) { return (2 + 4 * units + 7) & ~7; }
 
 __device__ __forceinline__ int pages_of(const int32_t* seq_lens, int b) { return (seq_lens[b] + 127) >> 7; }
 
 __device__ __forceinline__ int chunks_of(int pages, int ppc) { return (pages + ppc - 1) / ppc; }
 
+// Wavefront-wide inclusive scan with DPP (row shifts within 16-lane rows,
+// then row broadcasts), no LDS round trips.  ``Op`` is + or max over values
+// whose identity is 0.
 template <bool kMax>
-__device__ __forceinline__ int block_reduce(int v, int* sh) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) {
-    const int x = __shfl_xor(v, o, 64);
-    v = kMax ? max(v, x) : v + x;
-  }
-  __syncthreads();
-  if (wave_lane() == 0) sh[threadIdx.x >> 6] = v;
-  __syncthreads();
-  v = sh[0];
-#pragma unroll
-  for (int w = 1; w < kPlanThreads / 64; ++w) v = kMax ? max(v, sh[w]) : v + sh[w];
-  return v;
+__device__ __forceinline__ int dpp_op(int a, int b) {
+  return kMax ? max(a, b) : a + b;
+}
+template <bool kMax>
+__device__ __forceinline__ int wave_scan_dpp(int x) {
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true));  // row_shr:1
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true));  // row_shr:2
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true));  // row_shr:4
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true));  // row_shr:8
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return x;
+}
+template <bool kMax>
+__device__ __forceinline__ int wave_total(int x) {
+  return __builtin_amdgcn_readlane(wave_scan_dpp<kMax>(x), 63);
 }
 
-// Work plan, one workgroup.  Same policy and layout as the reference planner
+// Work plan.  Same policy and layout as the reference planner
 // (fused_attn_decode.cu:48-163): every sequence is cut into chunks of ``ppc``
-// pages, ``ppc`` the smallest for which the live rows fit ``budget`` units;
-// plan = [ppc, budget, (seq, first page) x units, (first unit, chunks) x B].
-__global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* seq_lens, int32_t* plan, int batch,
-                                                            int units, int kvh) {
-  __shared__ int sh[kPlanThreads / 64];
-  __shared__ int wtot[kPlanThreads / 64];
-  const int tid = threadIdx.x;
-  int total = 0, longest = 0, active = 0;
-  for (int b = tid; b < batch; b += kPlanThreads) {
-    const int n = pages_of(seq_lens, b);
-    total += n;
-    longest = max(longest, n);
-    active += n > 0;
+// pages, ``ppc`` the smallest for which the live rows fit ``budget`` units.
+// Wave 0 runs the search with the page counts in registers (one DPP
+// reduction per step, division by the uniform ``ppc`` via a reciprocal) and
+// writes each sequence's first unit; then every thread fills the descriptors
+// of its units in parallel, locating the sequence by binary search over the
+// first units (in LDS up to kPlanLds sequences).  The descriptors also carry
+// the first two block ids of each chunk.
+constexpr int kPlanCache = 16;  // page counts of batch <= 64 * 16 kept in registers
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanLds = 8192;
+
+struct Divider {  // x / d for 0 <= x < 2^24, 1 <= d
+  int d;
+  float inv;
+  __device__ explicit Divider(int d_) : d(d_), inv(1.0f / (float)d_) {}
+  __device__ __forceinline__ int div(int x) const {
+    int q = (int)((float)x * inv);
+    q += (q + 1) * d <= x;
+    q -= q * d > x;
+    return q;
   }
-  total = block_reduce<false>(total, sh);
-  longest = block_reduce<true>(longest, sh);
-  active = block_reduce<false>(active, sh);
-  const int capacity = max(1, units - batch + active);
-  const int wave = units - batch + 1;
-  int budget = min(capacity, max(active, wave));
-  if (capacity > budget) {
-    const int tail_bound = 2 * max(1, (total + budget - 1) / budget);
-    int c = 0;
-    for (int b = tid; b < batch; b += kPlanThreads) c += chunks_of(pages_of(seq_lens, b), tail_bound);
-    if (block_reduce<false>(c, sh) > budget) budget = capacity;
-  }
-  int lo = max(1, (total + budget - 1) / budget), hi = max(1, longest);
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    int c = 0;
-    for (int b = tid; b < batch; b += kPlanThreads) c += chunks_of(pages_of(seq_lens, b), mid);
-    if (block_reduce<false>(c, sh) <= budget)
-      hi = mid;
-    else
-      lo = mid + 1;
-  }
-  const int ppc = lo;
+  __device__ __forceinline__ int chunks(int pages) const { return div(pages + d - 1); }
+};
+
+__global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __restrict__ seq_lens,
+                                                            const int32_t* __restrict__ block_table, int64_t bt_stride,
+                                                            int32_t* __restrict__ plan, int batch, int units, int kvh) {
+  __shared__ int firsts[kPlanLds + 1];
+  __shared__ int shared_used, shared_ppc;
   int32_t* seq_plan = plan + 2 + 2 * units;
-  int used = 0;
-  for (int base = 0; base < batch; base += kPlanThreads) {
-    const int b = base + tid;
-    const int c = b < batch ? chunks_of(pages_of(seq_lens, b), ppc) : 0;
-    // block exclusive scan of c
-    const int incl = wave_incl_scan(c);
-    __syncthreads();
-    if (wave_lane() == 63) wtot[tid >> 6] = incl;
-    __syncthreads();
-    int first = incl - c, tile = 0;
-    for (int w = 0; w < kPlanThreads / 64; ++w) {
-      if (w < (tid >> 6)) first += wtot[w];
-      tile += wtot[w];
-    }
-    first += used;
-    if (b < batch) {
-      seq_plan[2 * b] = first;
-      seq_plan[2 * b + 1] = c;
-      const int seq = seq_lens[b], pages = pages_of(seq_lens, b);
-      for (int s = 0; s < c; ++s) {
-        plan[2 + 2 * (first + s)] = b;
-        plan[3 + 2 * (first + s)] = s * ppc;
-        int32_t* ud = plan + ud_offset(units) + 8 * (first + s);
-        ud[0] = b;
-        ud[1] = s * ppc;
-        ud[2] = min(pages, (s + 1) * ppc) - s * ppc;
-        ud[3] = seq;
-        ud[4] = first;
-        ud[5] = c;
+  const bool lds = batch <= kPlanLds;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int pg[kPlanCache];
+    int total = 0, longest = 0, active = 0;
+    static_for<0, kPlanCache>([&](auto k) {
+      pg[k] = 0;
+      if (64 * k < batch) {
+        const int b = lane + 64 * k;
+        pg[k] = b < batch ? pages_of(seq_lens, b) : 0;
+        total += pg[k];
+        longest = max(longest, pg[k]);
+        active += pg[k] > 0;
       }
+    });
+    for (int b = lane + 64 * kPlanCache; b < batch; b += 64) {
+      const int n = pages_of(seq_lens, b);
+      total += n;
+      longest = max(longest, n);
+      active += n > 0;
     }
-    used += tile;
+    total = wave_total<false>(total);
+    longest = wave_total<true>(longest);
+    active = wave_total<false>(active);
+    auto count_chunks = [&](int ppc) {
+      const Divider dv(ppc);
+      int c = 0;
+      static_for<0, kPlanCache>([&](auto k) {
+        if (64 * k < batch) c += dv.chunks(pg[k]);
+      });
+      for (int b = lane + 64 * kPlanCache; b < batch; b += 64) c += dv.chunks(pages_of(seq_lens, b));
+      return wave_total<false>(c);
+    };
+    const int capacity = max(1, units - batch + active);
+    const int wave = units - batch + 1;
+    int budget = min(capacity, max(active, wave));
+    if (capacity > budget) {
+      const int tail_bound = 2 * max(1, (total + budget - 1) / budget);
+      if (count_chunks(tail_bound) > budget) budget = capacity;
+    }
+    int lo = max(1, (total + budget - 1) / budget), hi = max(1, longest);
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (count_chunks(mid) <= budget)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    const int ppc = lo;
+    const Divider dv(ppc);
+    int used = 0;
+    auto place = [&](int b, int n) {
+      const int c = dv.chunks(n);
+      const int incl = wave_scan_dpp<false>(c);
+      const int first = used + incl - c;
+      if (b < batch) {
+        seq_plan[2 * b] = first;
+        seq_plan[2 * b + 1] = c;
+        if (lds) firsts[b] = first;
+      }
+      used += __builtin_amdgcn_readlane(incl, 63);
+    };
+    static_for<0, kPlanCache>([&](auto k) {
+      if (64 * k < batch) place(lane + 64 * k, pg[k]);
+    });
+    for (int base = 64 * kPlanCache; base < batch; base += 64) {
+      const int b = base + lane;
+      place(b, b < batch ? pages_of(seq_lens, b) : 0);
+    }
+    if (lane == 0) {
+      if (lds) firsts[batch] = used;
+      shared_used = used;
+      shared_ppc = ppc;
+      plan[0] = ppc;
+      plan[1] = budget;
+    }
   }
-  for (int u = used + tid; u < units; u += kPlanThreads) {
-    plan[2 + 2 * u] = -1;
-    plan[ud_offset(units) + 8 * u] = -1;
+  __syncthreads();
+  const int used = shared_used, ppc = shared_ppc;
+  const int ud0 = ud_offset(units);
+  auto first_of = [&](int b) { return b == batch ? used : lds ? firsts[b] : seq_plan[2 * b]; };
+  for (int u = threadIdx.x; u < units; u += kPlanThreads) {
+    int4* ud = reinterpret_cast<int4*>(plan + ud0 + 8 * u);
+    if (u >= used) {
+      plan[2 + 2 * u] = -1;
+      plan[ud0 + 8 * u] = -1;
+      continue;
+    }
+    // the last sequence whose first unit is <= u owns u (empty sequences
+    // share their successor's first unit)
+    int lo = 0, hi = batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (first_of(mid) <= u)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int b = lo, first = first_of(b), c = first_of(b + 1) - first;
+    const int seq = seq_lens[b], n = (seq + 127) >> 7;
+    const int p0 = (u - first) * ppc, np = min(n, p0 + ppc) - p0;
+    const int32_t* bt = block_table + (int64_t)b * bt_stride;
+    plan[2 + 2 * u] = b;
+    plan[3 + 2 * u] = p0;
+    ud[0] = make_int4(b, p0, np, seq);
+    ud[1] = make_int4(first, c, bt[p0], np > 1 ? bt[p0 + 1] : 0);
   }
   // merge-group counters of the fused merge; the last arrival of a group
   // resets its counter, so zeroing is needed only here
-  for (int x = tid; x < units * kvh; x += kPlanThreads) plan[ud_offset(units) + 8 * units + x] = 0;
-  if (tid == 0) {
-    plan[0] = ppc;
-    plan[1] = budget;
-  }
+  for (int x = threadIdx.x; x < units * kvh; x += kPlanThreads) plan[ud0 + 8 * units + x] = 0;
 }
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
@@ -498,8 +562,17 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int b = uniform(ud[0]);
     if (b < 0) continue;
     const int p0 = uniform(ud[1]), npages = uniform(ud[2]), seq = uniform(ud[3]);
-    const int first = uniform(ud[4]), chunks = uniform(ud[5]);
+    const int first = uniform(ud[4]), chunks = uniform(ud[5]), blk0 = uniform(ud[6]);
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
+    // page 0's records straight from the descriptor's block id (one hop
+    // shorter than through the block table); the rest through load_meta
+    RecRef kr, vr;
+    {
+      const int64_t kidx = ((int64_t)blk0 * 2) * p.kvh + h;
+      const int64_t ka = uniform64(p.rec_addr[kidx]), va = uniform64(p.rec_addr[kidx + p.kvh]);
+      kr = make_ref((uint32_t)ka, (uint32_t)((uint64_t)ka >> 32), uniform(p.rec_len[kidx]));
+      vr = make_ref((uint32_t)va, (uint32_t)((uint64_t)va >> 32), uniform(p.rec_len[kidx + p.kvh]));
+    }
     PageMeta meta = load_meta(p, bt, 0, npages, h, lane);
 
     __syncthreads();  // the previous unit is done with every tile
@@ -521,7 +594,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 
     // page 0: dense K slab and both variable regions, staged before the loop
-    RecRef kr = page_ref(meta, 0, 0), vr = page_ref(meta, 0, 1);
     FP_STAMP(2);
     SlabBuf fk, fv;
     prefetch_dense(kr, w, nt, fk);
@@ -723,8 +795,8 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.done = plan + p.ud_off + 8 * units;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   if (replan) {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, plan, (int)batch, (int)units,
-                       (int)kv_heads);
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan, (int)batch,
+                       (int)units, (int)kv_heads);
     FP_LAUNCH_CHECK();
   }
   hipLaunchKernelGGL(attn_kernel, dim3((unsigned)units, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);

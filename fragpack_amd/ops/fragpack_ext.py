@@ -121,6 +121,7 @@ class Extension:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = _i32
+        self._fused = lib.fp_fused_decode
         lib.fp_last_error.restype = ctypes.c_char_p
         lib.fp_abi_version.restype = _i32
 
@@ -131,28 +132,31 @@ class Extension:
     # -- fused_decode (fragpack_ext.cpp:5-9, fused_attn_decode.cu:429-478) --
     def fused_decode(self, q, rec_addr, rec_len, plut, slut, block_table, seq_lens, opart, ml, plan, out,
                      units: int, replan: bool, scale: float, group: int = 8) -> None:
-        _check(q.dim() == 3 and q.size(2) == 128 and q.stride(2) == 1 and q.stride(1) == 128
-               and q.stride(0) % 2 == 0 and q.dtype == torch.bfloat16,
-               "q must be [B, H, 128] with contiguous heads")
-        _check(out.dim() == 3 and out.stride(2) == 1 and out.stride(1) == 128 and out.dtype == torch.bfloat16,
+        # one tuple read per tensor property: this runs once per decode layer
+        qsh, qst, ost, bst = q.shape, q.stride(), out.stride(), block_table.stride()
+        bf16, i32 = torch.bfloat16, torch.int32
+        _check(len(qsh) == 3 and qsh[2] == 128 and qst[2] == 1 and qst[1] == 128 and qst[0] % 2 == 0
+               and q.dtype == bf16, "q must be [B, H, 128] with contiguous heads")
+        _check(len(ost) == 3 and ost[2] == 1 and ost[1] == 128 and out.dtype == bf16 and out.shape[1] == qsh[1],
                "out must be [B, H, 128] with contiguous heads")
-        _check(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table rows must be contiguous")
-        _check(seq_lens.dtype == torch.int32, "seq_lens must be int32")
-        _check(rec_addr.dtype == torch.int64 and rec_len.dtype == torch.int32, "record tables must be int64 / int32")
-        _check(plan.dtype == torch.int32, "decode plan must be int32 with 2 + 4 * units + units * kv_heads elements")
+        _check(block_table.dtype == i32 and bst[1] == 1, "block_table rows must be contiguous")
+        _check(seq_lens.dtype == i32, "seq_lens must be int32")
+        _check(rec_addr.dtype == torch.int64 and rec_len.dtype == i32, "record tables must be int64 / int32")
+        _check(plan.dtype == i32, "decode plan must be int32 with 2 + 4 * units + units * kv_heads elements")
         _check(opart.dtype == torch.float32 and ml.dtype == torch.float32, "decode workspace must be float32")
-        B = q.size(0)
-        kvh = q.size(1) // group
-        _check(kvh * group == q.size(1) and out.size(1) == q.size(1), "query heads must be a multiple of the group")
+        B = qsh[0]
+        kvh = qsh[1] // group
+        _check(kvh * group == qsh[1], "query heads must be a multiple of the group")
         if B == 0:
             return
-        self._call(
-            "fp_fused_decode", _dev(q, "q"), q.stride(0), B, kvh, group, _dev(rec_addr, "rec_addr"),
-            _dev(rec_len, "rec_len"), _dev(plut, "plut"), _dev(slut, "slut"), _dev(block_table, "block_table"),
-            block_table.stride(0), _dev(seq_lens, "seq_lens"), _dev(opart, "opart"), opart.numel(),
-            _dev(ml, "ml"), ml.numel(), _dev(plan, "plan"), plan.numel(), _dev(out, "out"), out.stride(0),
-            int(units), int(bool(replan)), float(scale), _stream(q),
-        )
+        if self._fused(
+            _dev(q, "q"), qst[0], B, kvh, group, _dev(rec_addr, "rec_addr"), _dev(rec_len, "rec_len"),
+            _dev(plut, "plut"), _dev(slut, "slut"), _dev(block_table, "block_table"), bst[0],
+            _dev(seq_lens, "seq_lens"), _dev(opart, "opart"), opart.numel(), _dev(ml, "ml"), ml.numel(),
+            _dev(plan, "plan"), plan.numel(), _dev(out, "out"), ost[0], units, replan, scale,
+            torch.cuda.current_stream().cuda_stream,
+        ):
+            raise RuntimeError(f"fp_fused_decode: {self._lib.fp_last_error().decode()}")
 
     # -- store (fragpack_ext.cpp:11-39, hbm_kv.cu:669-734) --
     def hbm_prepare(self, *args) -> None:

@@ -169,3 +169,51 @@ def test_paged_attention_repetition_identity():
     p = np.exp(s - s.max(1, keepdims=True))
     want = (p / p.sum(1, keepdims=True)) @ v
     np.testing.assert_allclose(got, want, atol=1e-4, rtol=1e-4)
+
+
+def _brute_min_ppc(pages: np.ndarray, budget: int) -> int:
+    return next(p for p in range(1, int(pages.max(initial=0)) + 2) if ((pages + p - 1) // p).sum() <= budget)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_decode_plan_invariants(seed):
+    """The planner restatement against brute force: ppc is the smallest chunk
+    size whose chunks fit the budget, the budget lies between the live rows
+    and the capacity, and the unit map tiles every sequence's pages once."""
+    rng = np.random.default_rng(seed)
+    batch = int(rng.integers(1, 300))
+    lens = rng.integers(0, 40000, batch).astype(np.int32)
+    lens[rng.random(batch) < 0.2] = 0
+    units = batch + int(rng.integers(0, 600))
+    ppc, budget, unit_map, seq_map = oracle.decode_plan(lens, units)
+    pages = (lens.astype(np.int64) + 127) // 128
+    active = int((pages > 0).sum())
+    assert max(1, min(active, units - batch + 1)) <= budget <= max(1, units - batch + active)
+    assert ppc == _brute_min_ppc(pages, budget)
+    covered = np.zeros(int(pages.sum()), np.int64)
+    offs = np.concatenate([[0], np.cumsum(pages)])
+    for u, (b, p0) in enumerate(unit_map):
+        if b < 0:
+            assert u >= seq_map[:, 1].sum()
+            continue
+        assert seq_map[b, 0] <= u < seq_map[b, 0] + seq_map[b, 1]
+        n = min(int(pages[b]), p0 + ppc) - p0
+        assert n > 0
+        covered[offs[b] + p0 : offs[b] + p0 + n] += 1
+    assert np.all(covered == 1)
+
+
+def test_decode_plan_known_answers():
+    """Hand-computed plans.  4 x 64 pages with 195 units: budget 192 (one wave
+    of splits), tail bound 4 keeps it, smallest ppc with 4*ceil(64/ppc) <= 192
+    is 2.  Minimum units (one per row) give one chunk per live row.  An all-empty
+    batch of 5 rows with 7 units: capacity max(1, 7-5+0) = 2, no chunks."""
+    ppc, budget, unit_map, seq_map = oracle.decode_plan(np.full(4, 8192, np.int32), 195)
+    assert (ppc, budget) == (2, 192)
+    assert seq_map.tolist() == [[0, 32], [32, 32], [64, 32], [96, 32]]
+    assert unit_map[33].tolist() == [1, 2] and unit_map[128, 0] == -1
+    lens = np.array([300, 0, 9000, 1], np.int32)
+    ppc, budget, _, seq_map = oracle.decode_plan(lens, 4)
+    assert budget == 3 and ppc == 71 and seq_map[:, 1].tolist() == [1, 0, 1, 1]
+    ppc, budget, unit_map, seq_map = oracle.decode_plan(np.zeros(5, np.int32), 7)
+    assert budget == 2 and ppc == 1 and np.all(unit_map[:, 0] == -1) and not seq_map[:, 1].any()
