@@ -40,6 +40,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 
+#ifndef FP_ATTN_WAVES_PER_EU
+#define FP_ATTN_WAVES_PER_EU 3  // occupancy target of attn_kernel (VGPR budget 512 / 3)
+#endif
 constexpr int kWaves = 4;  // wavefronts per workgroup = slabs per record
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
 
@@ -374,33 +377,27 @@ __device__ __forceinline__ void patch_raw(const RecRef& r, uint2 v, int w, int l
   }
 }
 
-// Lanes (in MFMA lane order) whose kernel-order thread precedes this lane's:
-// natural index 32 hh + 4 g + c, lane 16 c + 8 hh + g.
-__device__ __forceinline__ uint64_t natural_below(int c, int hh, int g) {
-  uint64_t m = 0;
-  if (hh) m |= 0x00FF00FF00FF00FFull;
-  m |= (uint64_t)(((1u << g) - 1u) << (8 * hh)) * 0x0001000100010001ull;
-  for (int cc = 0; cc < c; ++cc) m |= 1ull << (16 * cc + 8 * hh + g);
-  return m;
-}
+// Byte addresses for ds_bpermute between lane order and kernel order
+// (natural index 32 hh + 4 g + c <-> lane 16 c + 8 hh + g): ``to_nat`` makes
+// lane i read the lane holding kernel-order thread i, ``from_nat`` makes a
+// lane read position ``nt``.
+struct NatPerm {
+  int to_nat, from_nat;
+};
 
-// Exclusive prefix (in kernel order) of ``cnt`` (0..64) over the wave, from
-// bit-sliced ballots: sum_b 2^b popcount(ballot_b & below).
-__device__ __forceinline__ int natural_prefix(int cnt, uint64_t below) {
-  int x = 0;
-#pragma unroll
-  for (int b = 0; b < 7; ++b) {
-    const uint64_t m = __ballot((cnt >> b) & 1);
-    if (m) x += __builtin_popcountll(m & below) << b;
-  }
-  return x;
+// Exclusive prefix (in kernel order) of ``cnt`` over the wave: counts moved
+// into kernel order, a DPP inclusive scan, and moved back.
+__device__ __forceinline__ int natural_prefix(int cnt, NatPerm np) {
+  const int y = __builtin_amdgcn_ds_bpermute(np.to_nat, cnt);
+  const int incl = wave_scan_dpp<false>(y);
+  return __builtin_amdgcn_ds_bpermute(np.from_nat, incl) - cnt;
 }
 
 // Decodes this lane's kernel-order thread ``nt`` of the wave's slab ``w`` of
 // record ``r`` (escapes staged in ``esc``, header in ``hdr``) and calls
 // pair(a, word 2a, word 2a + 1) for a = 0..3.
 template <typename Pair>
-__device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int w, int nt, uint64_t below,
+__device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int w, int nt, NatPerm np,
                                             const HeadLut& lut, const uint8_t* esc, const uint32_t* hdr,
                                             Pair&& pair) {
   uint4 prev;
@@ -416,7 +413,7 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
     return;
   }
   const int e0 = (int)(hdr[4 + w] & 0xFFFFu);  // esc_prefix[2 w]
-  const int excl = natural_prefix(thread_escapes(b), below);
+  const int excl = natural_prefix(thread_escapes(b), np);
   decode_words(b, esc, e0 + excl, lut.p0, lut.p1, emit);
 }
 
@@ -542,14 +539,14 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
   }
 }
 
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) attn_kernel(AttnParams p) {
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FP_ATTN_WAVES_PER_EU))) attn_kernel(AttnParams p) {
   __shared__ AttnShared sh;
   const int lane = wave_lane();
-  const int w = threadIdx.x >> 6;  // this wave's slab of every record
+  const int w = uniform((int)(threadIdx.x >> 6));  // this wave's slab of every record (wave-uniform)
   const int h = blockIdx.y;
   const int c = lane >> 4, hh = (lane >> 3) & 1, g = lane & 7;
   const int nt = 32 * hh + 4 * g + c;
-  const uint64_t below = natural_below(c, hh, g);
+  const NatPerm np{4 * lane_of_natural(lane), 4 * nt};
   const int n = lane & 15;  // MFMA column = query head within the group
   const int budget = uniform(p.plan[1]);
   const HeadLut klut = load_lut(p.plut, p.slut, h);
@@ -624,7 +621,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      decode_slab(kr, fk, w, nt, below, klut, sh.esc[par][0], sh.hdr[par][0],
+      decode_slab(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0],
                   [&](auto a, const uint4& w0, const uint4& w1) {
                     const uint4 qa = tile_frag(sh.qt, n, a, c);
                     s0 = mfma(a_frag(w0, w1, 0), qa, s0);
@@ -685,7 +682,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       FP_STAMP(6 + 5 * min(i, 4));
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
-      decode_slab(vr, fv, w, nt, below, vlut, sh.esc[par][1], sh.hdr[par][1],
+      decode_slab(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1],
                   [&](auto a, const uint4& w0, const uint4& w1) {
                     const uint4 pa = tile_frag(sh.pt, n, a, c);
                     o0 = mfma(a_frag(w0, w1, 0), pa, o0);

@@ -211,9 +211,8 @@ __device__ __forceinline__ uint32_t esc_bits(uint32_t sk) { return ((sk + 0x1111
 __device__ __forceinline__ uint32_t lut16(uint32_t sel, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
   const uint32_t s7 = sel & 0x07070707u;
   const uint32_t lo = perm(t1, t0, s7), hi = perm(t3, t2, s7);
-  const uint32_t m = (sel >> 3) & 0x01010101u;
-  const uint32_t mask = (m << 8) - m;  // 0xFF where bit 3 of the selector is set
-  return (hi & mask) | (lo & ~mask);
+  // byte k from lo (selector k) or hi (k + 4) by bit 3 of selector byte k
+  return perm(hi, lo, ((sel >> 1) & 0x04040404u) | 0x03020100u);
 }
 
 // Eight nibbles (escape stream order, low nibble first) -> eight bytes
@@ -285,7 +284,8 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
   static_for<0, 8>([&](auto st_c) {
     constexpr int st = decltype(st_c)::value;
     const uint32_t sk = sym_word(b, st);
-    const uint32_t eb = esc_bits(sk);
+    const uint32_t b8 = (sk + 0x11111111u) & 0x88888888u;  // bit 3 of each escape nibble
+    const uint32_t eb = b8 >> 3;
     // primary high bytes of scalars 0,2,4,6 / 1,3,5,7 (escape code 7 -> 0)
     const uint32_t hp_ev = perm(lut1, lut0, sk & 0x07070707u);
     const uint32_t hp_od = perm(lut1, lut0, (sk >> 4) & 0x07070707u);
@@ -297,7 +297,7 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
     eo += __builtin_popcount(eb);
     // selector nibble: exclusive escape rank for escapes, 0xC (-> 0x00) else
     const uint32_t rank = eb * 0x11111110u;
-    const uint32_t m15 = (eb << 4) - eb;
+    const uint32_t m15 = b8 | (b8 - eb);  // 0xF in escape nibbles (no multiply)
     const uint32_t sel = (rank & m15) | (~m15 & 0xCCCCCCCCu);
     const uint32_t h_ev = hp_ev | perm(ehi, elo, sel & 0x0F0F0F0Fu);
     const uint32_t h_od = hp_od | perm(ehi, elo, (sel >> 4) & 0x0F0F0F0Fu);
@@ -313,7 +313,8 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
 // Escape count of one thread's 64 scalars.
 __device__ __forceinline__ int thread_escapes(const SlabBuf& b) {
   int n = 0;
-  static_for<0, 8>([&](auto st) { n += __builtin_popcount(esc_bits(sym_word(b, st))); });
+  // same expression as decode_words' escape bits, so the two share it
+  static_for<0, 8>([&](auto st) { n += __builtin_popcount((sym_word(b, st) + 0x11111111u) & 0x88888888u); });
   return n;
 }
 
