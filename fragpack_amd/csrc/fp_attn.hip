@@ -43,7 +43,8 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 #ifndef FP_ATTN_WAVES_PER_EU
 #define FP_ATTN_WAVES_PER_EU 3  // occupancy target of attn_kernel (VGPR budget 512 / 3)
 #endif
-constexpr int kWaves = 4;  // wavefronts per workgroup = slabs per record
+constexpr int kWaves = 4;
+constexpr float kLazyMax = 8.f;  // log2 headroom of the speculative softmax reference  // wavefronts per workgroup = slabs per record
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
 
 struct AttnParams {
@@ -639,46 +640,61 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
       if (lane < 8) sh.red[w][lane] = mloc;
+      // Softmax against the running max m_run, speculatively: the page max is
+      // known only after the barrier.  P = exp2(s - m_run) stays exact while
+      // the page max exceeds m_run by at most kLazyMax (P <= 2^kLazyMax);
+      // otherwise (and on the first page) P is recomputed below with a new
+      // reference max, at the cost of one more barrier.
+      float e0[4], e1[4], psum = 0.f;
+      const bool spec = m_run != -INFINITY;  // the same in every wave
+      auto softmax_tile = [&](float m_ref) {
+        psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          e0[r] = __builtin_amdgcn_exp2f(s0[r] - m_ref);
+          e1[r] = __builtin_amdgcn_exp2f(s1[r] - m_ref);
+          psum += e0[r] + e1[r];
+        }
+        // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
+        if (hh == 0) {
+          uint8_t* base = sh.pt + ((n * 4 + w) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1);
+          auto pk = [](float x, float y) {
+            return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
+          };
+          *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e0[1]);
+          *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e0[3]);
+          *reinterpret_cast<uint32_t*>(base + 4) = pk(e1[0], e1[1]);
+          *reinterpret_cast<uint32_t*>(base + 20) = pk(e1[2], e1[3]);
+        }
+      };
+      if (spec) softmax_tile(m_run);
       FP_STAMP(4 + 5 * min(i, 4));
       if (more) {
         prefetch_dense(nkr, w, nt, fk);
         expand_var(nkr, vk, w, lane, klut.s, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
         expand_var(nvr, vv, w, lane, vlut.s, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
       }
-      __syncthreads();  // B2: page max per wave known; next page's escapes expanded
+      __syncthreads();  // B2: page max per wave known; P tile written; next page's escapes expanded
       FP_STAMP(5 + 5 * min(i, 4));
-      float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
-      const float m_new = fmaxf(m_run, mpage);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      m_run = m_new;
-      float e0[4], e1[4], psum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        e0[r] = __builtin_amdgcn_exp2f(s0[r] - m_use);
-        e1[r] = __builtin_amdgcn_exp2f(s1[r] - m_use);
-        psum += e0[r] + e1[r];
+      const float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
+      // the same decision in every wave: all read the same page maxima
+      if (!spec || __ballot(mpage > m_run + kLazyMax) != 0) {
+        const float m_new = fmaxf(m_run, mpage);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        l_run *= alpha;
+        o0 *= alpha;
+        o1 *= alpha;
+        softmax_tile(m_use);
+        __syncthreads();  // rewritten P tile complete
       }
-      l_run = l_run * alpha + psum;
-      o0 *= alpha;
-      o1 *= alpha;
-      // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
-      if (hh == 0) {
-        uint8_t* base = sh.pt + ((n * 4 + w) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1);
-        auto pk = [](float x, float y) {
-          return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) |
-                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
-        };
-        *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e0[1]);
-        *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e0[3]);
-        *reinterpret_cast<uint32_t*>(base + 4) = pk(e1[0], e1[1]);
-        *reinterpret_cast<uint32_t*>(base + 20) = pk(e1[2], e1[3]);
-      }
+      l_run += psum;
       if (more) {
         patch_raw(nkr, vk, w, lane, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
         patch_raw(nvr, vv, w, lane, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
       }
-      __syncthreads();  // B3: P tile complete
       FP_STAMP(6 + 5 * min(i, 4));
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
