@@ -122,7 +122,11 @@ def reference_decode(torch, q, kv, block_table, lens, heads, group, scale):
     return out
 
 
-def decode_bench(torch, args) -> dict:
+def decode_bench(torch, args, raw: bool = False) -> dict:
+    """One decode step (plan + attention) over a filled store.  ``raw``: the
+    BF16 paged baseline arm -- tables whose 22 high bytes never occur in the
+    data (0x00..0x15), so every record falls back to its raw 32 KB form and
+    the same kernel streams plain BF16 pages."""
     from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
 
     B, H, G, ctx = args.batch, args.heads, args.group, args.context
@@ -131,10 +135,15 @@ def decode_bench(torch, args) -> dict:
     tables = calibrated_tables(rng, H, scales)
     pages = math.ceil(ctx / T)
     nb = B * pages
+    overflow = 8192
+    if raw:
+        tables = np.broadcast_to(np.arange(22, dtype=np.uint8), tables.shape).copy()
+        overflow = nb * 2 * H + 64
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
     scales_t = torch.from_numpy(scales).float().cuda()
     t0 = time.time()
-    store, arena, kv = build_store(torch, H, nb, tables, gen, scales_t, fill_blocks=64, keep_kv=True)
+    store, arena, kv = build_store(torch, H, nb, tables, gen, scales_t, fill_blocks=64, keep_kv=True,
+                                   overflow=overflow)
     log(f"store filled: {nb} blocks x {2 * H} records in {time.time() - t0:.1f}s, stats {store.stats()}")
     perm = torch.from_numpy(rng.permutation(nb).astype(np.int32)).cuda()
     bt = perm.view(B, pages).contiguous()
@@ -193,10 +202,18 @@ def decode_bench(torch, args) -> dict:
     step_ms = timed(step)
     # the attention kernel alone (replan=False launches only attn_kernel)
     kern_ms = timed(lambda: step(False))
+    # the same step captured once and replayed as a HIP graph
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        step(True)
+    graph.replay()
+    graph_ms = timed(graph.replay)
     comp_ratio = rec_bytes / (2 * used.size * H * 32768)
     log(f"step {step_ms * 1e3:.1f} us, attn kernel {kern_ms * 1e3:.1f} us, "
         f"compressed {rec_bytes / 1e6:.1f} MB ({comp_ratio:.3f} of raw), effective BF16 {eff_bytes / 1e6:.1f} MB")
-    return dict(step_ms=step_ms, kern_ms=kern_ms, algo_bytes=algo_bytes, eff_bytes=eff_bytes, rec_bytes=rec_bytes,
+    return dict(step_ms=step_ms, kern_ms=kern_ms, graph_ms=graph_ms, algo_bytes=algo_bytes, eff_bytes=eff_bytes, rec_bytes=rec_bytes,
                 valid=valid, units=units, store=store, arena=arena, bt=bt, lens=lens, q=q, tables=tables,
                 scale=scale, comp_ratio=comp_ratio, max_err=err.max().item())
 
@@ -325,6 +342,7 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-encode", action="store_true")
+    ap.add_argument("--no-raw-arm", action="store_true", help="skip the all-raw (BF16 paged) comparison arm")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3x (scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -349,6 +367,12 @@ def main() -> None:
     res = decode_bench(torch, args)
     enc = None if args.no_encode else encode_bench(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(torch, res, args)
+    raw = None
+    if not args.no_raw_arm:
+        for k in ("store", "arena"):
+            res.pop(k)
+        torch.cuda.empty_cache()
+        raw = decode_bench(torch, args, raw=True)
     step_s = res["step_ms"] / 1e3
     kern_s = res["kern_ms"] / 1e3
     achieved = res["algo_bytes"] / kern_s / 1e9
@@ -372,6 +396,7 @@ def main() -> None:
         "config": {"workload": "config 1: decode step, B4 x H4 x G8 x 8192 ctx, head_dim 128, one layer",
                    "batch": args.batch, "kv_heads": args.heads, "gqa": args.group, "context": args.context,
                    "units": res["units"]},
+        "graph_us_per_step": round(res["graph_ms"] * 1e3, 2),
         "compressed_GBps": round(res["algo_bytes"] / step_s / 1e9, 2),
         "compression": round(res["comp_ratio"], 4),
         "validated": res["valid"],
@@ -382,6 +407,12 @@ def main() -> None:
                      "algo_bytes_per_launch": res["algo_bytes"]},
         "cpu_baseline": cpu,
     }
+    if raw is not None:
+        line["bf16_paged_arm"] = {
+            "what": "same step over all-raw records (every record 32 KB BF16: the paged BF16 baseline)",
+            "us_per_step": round(raw["step_ms"] * 1e3, 2), "kernel_us": round(raw["kern_ms"] * 1e3, 2),
+            "validated": raw["valid"], "compressed_step_speedup": round(raw["step_ms"] / res["step_ms"], 3),
+            "hbm_GBps": round(raw["algo_bytes"] / (raw["kern_ms"] / 1e3) / 1e9, 1)}
     if enc is not None:
         line["encode"] = {"workload": f"config 3 shape: {args.encode_blocks} blocks x 8 KV heads x K/V, 10% "
                                       "Student-t(2)x16, overflow 8192",

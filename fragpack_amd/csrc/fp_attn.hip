@@ -9,9 +9,11 @@
 //   of pages of one (sequence, KV head) with an online softmax.  Per page,
 //   wave w decodes slab w (kernel-order threads 64w..64w+63) of the K record
 //   -- tokens 32w..32w+31 -- and then slab w of the V record -- dims
-//   32w..32w+31 --, so a page costs each wave two decode passes.  Three
-//   workgroup barriers per page: variable region staged, page max known, P
-//   tile complete.
+//   32w..32w+31 --, so a page costs each wave two decode passes.  Two
+//   workgroup barriers per page: (1) escapes staged and the previous page's
+//   V pass done, (2) page maxima known and P tile written (the softmax runs
+//   speculatively against the running max; a third barrier only when the
+//   page max outruns it).
 // * Lane l decodes kernel-order thread nt = 32 hh + 4 g + c of its slab, with
 //   c = l >> 4, hh = (l >> 3) & 1, g = l & 7.  With that assignment the
 //   decoded words are directly the A operands of v_mfma_f32_16x16x32_bf16:
@@ -43,8 +45,8 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 #ifndef FP_ATTN_WAVES_PER_EU
 #define FP_ATTN_WAVES_PER_EU 3  // occupancy target of attn_kernel (VGPR budget 512 / 3)
 #endif
-constexpr int kWaves = 4;
-constexpr float kLazyMax = 8.f;  // log2 headroom of the speculative softmax reference  // wavefronts per workgroup = slabs per record
+constexpr int kWaves = 4;          // wavefronts per workgroup = slabs per record
+constexpr float kLazyMax = 8.f;    // log2 headroom of the speculative softmax reference
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
 
 struct AttnParams {

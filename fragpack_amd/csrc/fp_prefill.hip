@@ -1,0 +1,332 @@
+// Causal varlen prefill attention over the paged BF16 workspace (gfx950).
+//
+// Reference path: the vLLM FlashAttention call of the FragPack backend
+// (fragpack/integrations/vllm/backend.py:560-575, prefill groups :387-444):
+// flash_attn_varlen_func(q, k = wk, v = wv, out, cu_seqlens_q, max_seqlen_q,
+// seqused_k, max_seqlen_k, softmax_scale, causal=True, block_table).  The
+// workspace is what HbmKvStore.gather writes: token-major BF16
+// [pages, 128, H, 128]; sequence b's key j lives in page
+// block_table[b][j / 128], row j % 128.  Queries are the last
+// q_len = cu[b+1] - cu[b] positions of the sequence (causal mask aligned
+// bottom-right: query i sees keys j <= i + seqused_k - q_len).
+//
+// Design (MI355X):
+// * One 256-thread workgroup (4 wavefronts) per (128-row query tile, KV head).
+//   The 128 rows are T = 128 / G tokens x G query heads of the KV head
+//   (head-major), so every K / V tile read from HBM serves the whole GQA
+//   group.  Wave w owns rows 32w .. 32w + 31 as two 16-column MFMA tiles.
+// * Keys stream in 64-key tiles through double-buffered LDS: K row-major
+//   (padded rows), V transposed to [dim][key] on the way in, so both MFMA
+//   A operands are contiguous LDS reads.
+// * S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_16x16x32_bf16.  The
+//   accumulator layout of S^T (lane = query column, 4 consecutive keys per
+//   16-lane group) is, after BF16 packing, exactly the B operand of the PV
+//   product once the PV contraction visits keys in the matching order
+//   {4q..4q+3, 16+4q..16+4q+3} -- P never leaves registers.
+// * Online softmax in the log2 domain (exp2), P rounded to BF16 for PV while
+//   l sums the fp32 P -- the arithmetic FlashAttention uses.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/fragpack_hip.h"
+#include "fp_capi_internal.hpp"
+
+namespace fp {
+namespace {
+
+typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPfRows = 128;       // query rows (token x head) per workgroup
+constexpr int kPfKeys = 64;        // keys per LDS tile
+constexpr int kPfDim = 128;
+constexpr int kKRow = 272;         // LDS bytes per K row (256 + 16 pad)
+constexpr int kVRow = 136;         // LDS bytes per V^T row (128 + 8 pad)
+constexpr int kKBytes = kPfKeys * kKRow;   // 17408
+constexpr int kVBytes = kPfDim * kVRow;    // 17408
+constexpr int kStageBytes = kKBytes + kVBytes;
+
+struct PrefillParams {
+  const uint16_t* q;
+  const uint16_t* wk;
+  const uint16_t* wv;
+  const int32_t* cu_q;
+  const int32_t* seq_k;
+  const int32_t* block_table;
+  uint16_t* out;
+  int64_t q_stride;    // elements between consecutive query tokens
+  int64_t out_stride;  // elements between consecutive output tokens
+  int64_t bt_stride;
+  int64_t num_pages;
+  int kvh, group, num_seqs, tiles_per_seq;
+  float scale_log2;
+  int causal;
+};
+
+__device__ __forceinline__ pf_f32x4 pf_mfma(const uint4& a, const uint4& b, pf_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pf_bf16x8, a), __builtin_bit_cast(pf_bf16x8, b),
+                                                  c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
+}
+
+__device__ __forceinline__ uint32_t pf_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Global -> register staging of one 64-key tile: thread t holds K chunks
+// (key 16i + t / 16, dims 8 (t % 16) ..) and V chunks (keys 4 (t / 16) + i,
+// same dims), i = 0..3.
+struct TileRegs {
+  uint4 k[4];
+  uint4 v[4];
+};
+
+__device__ __forceinline__ const uint16_t* key_row(const PrefillParams& p, const int32_t* bt, int key, int h,
+                                                   const uint16_t* base) {
+  const int64_t page = bt[key >> 7];
+  return base + ((page * 128 + (key & 127)) * p.kvh + h) * kPfDim;
+}
+
+__device__ __forceinline__ void load_tile(const PrefillParams& p, const int32_t* bt, int key0, int nkeys, int h,
+                                          TileRegs& r) {
+  const int t = threadIdx.x;
+  const int dc = t & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kk = 16 * i + (t >> 4);
+    r.k[i] = kk < nkeys ? *reinterpret_cast<const uint4*>(key_row(p, bt, key0 + kk, h, p.wk) + 8 * dc)
+                        : make_uint4(0u, 0u, 0u, 0u);
+    const int kv = 4 * (t >> 4) + i;
+    r.v[i] = kv < nkeys ? *reinterpret_cast<const uint4*>(key_row(p, bt, key0 + kv, h, p.wv) + 8 * dc)
+                        : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// Registers -> LDS stage: K rows as they are, V transposed (8-byte writes of
+// four consecutive keys of one dim).
+__device__ __forceinline__ void store_tile(uint8_t* stage, const TileRegs& r) {
+  const int t = threadIdx.x;
+  const int dc = t & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<uint4*>(stage + (16 * i + (t >> 4)) * kKRow + 16 * dc) = r.k[i];
+  uint8_t* vt = stage + kKBytes;
+  const int kg = t >> 4;  // keys 4 kg .. 4 kg + 3
+  auto dw = [&](int i, int e) { return e == 0 ? r.v[i].x : e == 1 ? r.v[i].y : e == 2 ? r.v[i].z : r.v[i].w; };
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t a = dw(0, e), b = dw(1, e), c = dw(2, e), d = dw(3, e);
+    // dims 8 dc + 2e (low halves) and 8 dc + 2e + 1 (high halves)
+    const uint2 lo = make_uint2(pf_perm(b, a, 0x05040100u), pf_perm(d, c, 0x05040100u));
+    const uint2 hi = make_uint2(pf_perm(b, a, 0x07060302u), pf_perm(d, c, 0x07060302u));
+    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e) * kVRow + 8 * kg) = lo;
+    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e + 1) * kVRow + 8 * kg) = hi;
+  }
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillParams p) {
+  extern __shared__ __align__(16) uint8_t pf_smem[];
+  const int h = blockIdx.y;
+  // longest query tiles first: later tiles see more keys under the causal mask
+  const int b = blockIdx.x % p.num_seqs;
+  const int qtile = p.tiles_per_seq - 1 - (int)(blockIdx.x / p.num_seqs);
+  const int q0 = p.cu_q[b], qlen = p.cu_q[b + 1] - q0;
+  const int T = kPfRows / p.group;  // query tokens per tile
+  const int t0 = qtile * T;
+  if (t0 >= qlen) return;
+  const int klen = p.seq_k[b];
+  const int shift = klen - qlen;  // query i sees keys <= i + shift (causal)
+  const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride;
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, q4 = lane >> 4;
+  // this lane's two query columns (tiles qt = 0, 1): row -> (head g, token t)
+  int tok[2], hq[2];
+  bool rvalid[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int row = 32 * w + 16 * qt + j;
+    const int g = row / T, t = row - g * T;
+    tok[qt] = t0 + t;
+    hq[qt] = h * p.group + g;
+    rvalid[qt] = tok[qt] < qlen;
+  }
+  // Q^T fragments (B operands): lane (j, q4) holds dims 32 ks + 8 q4 .. + 7
+  uint4 qf[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const uint16_t* qrow = p.q + (int64_t)(q0 + (rvalid[qt] ? tok[qt] : 0)) * p.q_stride + (int64_t)hq[qt] * kPfDim;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[qt][ks] = rvalid[qt] ? *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * q4) : make_uint4(0u, 0u, 0u, 0u);
+  }
+  // keys this tile needs: up to the last valid query's causal limit
+  const int last_tok = min(t0 + T, qlen) - 1;
+  const int kend = p.causal ? min(klen, last_tok + shift + 1) : klen;
+  const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
+  // causal limit per query column
+  int kmax[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) kmax[qt] = p.causal ? min(klen, tok[qt] + shift + 1) : klen;
+
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  pf_f32x4 o[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  TileRegs regs;
+  if (ntiles > 0) {
+    load_tile(p, bt, 0, min(kPfKeys, kend), h, regs);
+    store_tile(pf_smem, regs);
+  }
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int key0 = it * kPfKeys;
+    const uint8_t* stage = pf_smem + (it & 1) * kStageBytes;
+    const bool more = it + 1 < ntiles;
+    if (more) load_tile(p, bt, key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, regs);
+
+    // ---- S^T = K Q^T: s[kt][qt], keys key0 + 16 kt + 4 q4 + r ----
+    pf_f32x4 s[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt][0] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+      s[kt][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(stage + (16 * kt + j) * kKRow + 64 * ks + 16 * q4);
+        s[kt][0] = pf_mfma(kf, qf[0][ks], s[kt][0]);
+        s[kt][1] = pf_mfma(kf, qf[1][ks], s[kt][1]);
+      }
+    }
+    // ---- mask, online softmax, P^T fragments ----
+    const bool edge = key0 + kPfKeys > min(kmax[0], kmax[1]);  // wave-uniform enough; exact test below
+    uint4 pf[2][2];  // [kk][qt]
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = s[kt][qt][r] * p.scale_log2;
+          if (edge && key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) x = -INFINITY;
+          s[kt][qt][r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m[qt], mloc);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
+      m[qt] = m_new;
+      float psum = 0.f;
+      float e[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          e[kt][r] = __builtin_amdgcn_exp2f(s[kt][qt][r] - m_use);
+          psum += e[kt][r];
+        }
+      l[qt] = l[qt] * alpha + psum;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+      // B operand of k-step kk: keys 32 kk + {4 q4 .. 4 q4 + 3} (tile 2 kk) and
+      // 32 kk + 16 + {4 q4 ..} (tile 2 kk + 1)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        pf[kk][qt] = make_uint4(pk_bf16(e[2 * kk][0], e[2 * kk][1]), pk_bf16(e[2 * kk][2], e[2 * kk][3]),
+                                pk_bf16(e[2 * kk + 1][0], e[2 * kk + 1][1]), pk_bf16(e[2 * kk + 1][2], e[2 * kk + 1][3]));
+    }
+    // ---- O^T += V^T P^T: o[dt][qt], dims 16 dt + 4 q4 + r ----
+    const uint8_t* vt = stage + kKBytes;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint8_t* vrow = vt + (16 * dt + j) * kVRow;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 2 * (32 * kk + 4 * q4));
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 2 * (32 * kk + 16 + 4 * q4));
+        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        o[dt][0] = pf_mfma(vf, pf[kk][0], o[dt][0]);
+        o[dt][1] = pf_mfma(vf, pf[kk][1], o[dt][1]);
+      }
+    }
+    if (more) store_tile(pf_smem + ((it + 1) & 1) * kStageBytes, regs);
+    __syncthreads();
+  }
+  // ---- normalise and store: lane holds dims 16 dt + 4 q4 + r of query j ----
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float lt = l[qt];
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    if (!rvalid[qt]) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t* orow = p.out + (int64_t)(q0 + tok[qt]) * p.out_stride + (int64_t)hq[qt] * kPfDim;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * q4) =
+          make_uint2(pk_bf16(o[dt][qt][0] * inv, o[dt][qt][1] * inv), pk_bf16(o[dt][qt][2] * inv, o[dt][qt][3] * inv));
+  }
+}
+
+}  // namespace
+}  // namespace fp
+
+using namespace fp;
+
+extern "C" int fp_prefill_attention(const void* q, int64_t q_stride, const void* wk, const void* wv, int64_t num_pages,
+                                    int64_t kv_heads, int64_t group, const int32_t* cu_seqlens_q,
+                                    const int32_t* seqused_k, const int32_t* block_table, int64_t bt_stride,
+                                    int64_t num_seqs, int64_t max_seqlen_q, int64_t max_seqlen_k, double scale,
+                                    int causal, void* out, int64_t out_stride, fp_stream_t stream) {
+  FP_CHECK(num_seqs >= 0 && max_seqlen_q >= 0 && max_seqlen_k >= 0, "negative sizes");
+  if (num_seqs == 0 || max_seqlen_q == 0) return 0;
+  FP_CHECK(group == 1 || group == 2 || group == 4 || group == 8, "query heads per KV head must be 1, 2, 4 or 8");
+  FP_CHECK(kv_heads >= 1 && kv_heads <= 65535, "kv_heads out of range");
+  FP_CHECK(q && wk && wv && cu_seqlens_q && seqused_k && block_table && out, "null pointer");
+  FP_CHECK(q_stride >= kv_heads * group * kPfDim && out_stride >= kv_heads * group * kPfDim,
+           "token strides must cover all query heads");
+  FP_CHECK(bt_stride >= (max_seqlen_k + 127) / 128, "block table narrower than max_seqlen_k");
+  FP_CHECK(((uintptr_t)q | (uintptr_t)out | (uintptr_t)wk | (uintptr_t)wv) % 16 == 0 && q_stride % 8 == 0 &&
+               out_stride % 8 == 0,
+           "q / out / workspace must be 16-byte aligned with 8-element token strides");
+  const int64_t rows_per_tile = kPfRows / group;
+  const int64_t tiles = (max_seqlen_q + rows_per_tile - 1) / rows_per_tile;
+  FP_CHECK(tiles * num_seqs < (1LL << 31), "grid too large");
+  PrefillParams p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.wk = static_cast<const uint16_t*>(wk);
+  p.wv = static_cast<const uint16_t*>(wv);
+  p.cu_q = cu_seqlens_q;
+  p.seq_k = seqused_k;
+  p.block_table = block_table;
+  p.out = static_cast<uint16_t*>(out);
+  p.q_stride = q_stride;
+  p.out_stride = out_stride;
+  p.bt_stride = bt_stride;
+  p.num_pages = num_pages;
+  p.kvh = (int)kv_heads;
+  p.group = (int)group;
+  p.num_seqs = (int)num_seqs;
+  p.tiles_per_seq = (int)tiles;
+  p.scale_log2 = (float)(scale * 1.4426950408889634);
+  p.causal = causal ? 1 : 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // two 34 KB stages exceed the default 64 KB dynamic LDS limit
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
+  FP_CHECK(attr == hipSuccess, "cannot raise the prefill kernel's LDS limit");
+  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(tiles * num_seqs), (unsigned)kv_heads), dim3(256),
+                     2 * kStageBytes, s, p);
+  FP_LAUNCH_CHECK();
+  return 0;
+}

@@ -116,6 +116,8 @@ class Extension:
             "fp_hbm_import": [sp, _p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p],
             "fp_encode_records": [_p, _i64, _p, _p, _p, _i64, _p, _p, _p],
             "fp_decode_records": [_p, _p, _i64, _p, _p, _p, _p, _i64, _p, _p],
+            "fp_prefill_attention": [_p, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _f64,
+                                     _i32, _p, _i64, _p],
         }
         for name, args in sigs.items():
             fn = getattr(lib, name)
@@ -264,6 +266,31 @@ class Extension:
         self._call("fp_decode_records", _dev(rec_addr, "rec_addr"), _dev(rec_len, "rec_len"), n, _dev(kv, "kv"),
                    _dev(plut, "plut"), _dev(slut, "slut"), _dev(tab_idx, "tab_idx"), slut.numel() // 16,
                    _dev(out, "out"), _stream(out))
+
+    # -- prefill (the FlashAttention call of backend.py:560-575) --
+    def prefill_attention(self, q, wk, wv, out, cu_seqlens_q, seqused_k, block_table, max_seqlen_q: int,
+                          max_seqlen_k: int, scale: float, causal: bool) -> None:
+        n_seqs = seqused_k.numel()
+        if n_seqs == 0 or q.size(0) == 0:
+            return
+        _check(q.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and wk.dtype == torch.bfloat16
+               and wv.dtype == torch.bfloat16, "q / k / v / out must be BF16")
+        _check(q.dim() == 3 and q.size(2) == 128 and q.stride(2) == 1 and q.stride(1) == 128,
+               "q must be [N, Hq, 128] with contiguous heads")
+        _check(out.shape == q.shape and out.stride(2) == 1 and out.stride(1) == 128, "out must match q")
+        _check(wk.dim() == 4 and wk.size(1) == 128 and wk.size(3) == 128 and wk.is_contiguous()
+               and wv.shape == wk.shape and wv.is_contiguous(), "k / v must be contiguous [P, 128, H, 128]")
+        kvh = wk.size(2)
+        group = q.size(1) // kvh
+        _check(group * kvh == q.size(1), "query heads must be a multiple of the KV heads")
+        _check(cu_seqlens_q.dtype == torch.int32 and seqused_k.dtype == torch.int32
+               and cu_seqlens_q.numel() == n_seqs + 1, "cu_seqlens_q int32 [B + 1], seqused_k int32 [B]")
+        _check(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1
+               and block_table.size(0) == n_seqs, "block_table must be int32 [B, pages] with contiguous rows")
+        self._call("fp_prefill_attention", _dev(q, "q"), q.stride(0), _dev(wk, "k"), _dev(wv, "v"), wk.size(0), kvh,
+                   group, _dev(cu_seqlens_q, "cu_seqlens_q"), _dev(seqused_k, "seqused_k"),
+                   _dev(block_table, "block_table"), block_table.stride(0), n_seqs, int(max_seqlen_q),
+                   int(max_seqlen_k), float(scale), int(bool(causal)), _dev(out, "out"), out.stride(0), _stream(q))
 
 
 @functools.cache

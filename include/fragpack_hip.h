@@ -133,6 +133,26 @@ int fp_decode_records(const int64_t* rec_addr, const int32_t* rec_len, int64_t n
                       const uint32_t* plut, const uint8_t* slut, const int32_t* tab_idx, int64_t n_tables,
                       void* out, fp_stream_t stream);
 
+/*
+ * Causal varlen prefill attention over the paged BF16 workspace (the
+ * workspace HbmKvStore.gather fills): replaces the vLLM FlashAttention call
+ * flash_attn_varlen_func(q, k, v, out, cu_seqlens_q, max_seqlen_q,
+ * seqused_k, max_seqlen_k, softmax_scale, causal=True, block_table) of
+ * fragpack/integrations/vllm/backend.py:560-575.
+ *   q, out: BF16 [Nq, kv_heads * group, 128], heads contiguous, token
+ *     strides q_stride / out_stride (elements).
+ *   wk, wv: BF16 [num_pages, 128, kv_heads, 128]; sequence b's key j is row
+ *     j % 128 of page block_table[b * bt_stride + j / 128].
+ *   cu_seqlens_q int32 [num_seqs + 1]; seqused_k int32 [num_seqs] (>= the
+ *     sequence's query count: queries are its last positions, causal mask
+ *     aligned bottom-right).  group in {1, 2, 4, 8}.
+ */
+int fp_prefill_attention(const void* q, int64_t q_stride, const void* wk, const void* wv, int64_t num_pages,
+                         int64_t kv_heads, int64_t group, const int32_t* cu_seqlens_q, const int32_t* seqused_k,
+                         const int32_t* block_table, int64_t bt_stride, int64_t num_seqs, int64_t max_seqlen_q,
+                         int64_t max_seqlen_k, double scale, int causal, void* out, int64_t out_stride,
+                         fp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
