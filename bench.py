@@ -39,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 T = 128
 D = 128
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 DENSE = 22528
 
 
@@ -218,6 +219,60 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
                 scale=scale, comp_ratio=comp_ratio, max_err=err.max().item())
 
 
+def prefill_bench(torch, args) -> dict:
+    """Causal prefill over config 4's prompts: ``--prefill-seqs`` x
+    ``--prefill-len`` tokens, 32 query heads over 8 KV heads (GQA 4), on a
+    paged BF16 workspace (pages in permuted order).  FLOPs = 4 * D * Hq *
+    sum over queries of the keys it sees (QK^T and PV, 2 flops per MAC).
+    Checked against an fp32 reference on a sample of query rows."""
+    from fragpack_amd.ops.prefill_attn import flash_attn_varlen_func
+
+    S, L, H, G = args.prefill_seqs, args.prefill_len, 8, 4
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 4)
+    pages_per = math.ceil(L / T)
+    n_pages = S * pages_per
+    rng = np.random.default_rng(args.seed + 4)
+    bt = torch.from_numpy(rng.permutation(n_pages).astype(np.int32).reshape(S, pages_per)).cuda()
+    wk = torch.randn((n_pages, T, H, D), generator=gen, device="cuda").to(torch.bfloat16)
+    wv = torch.randn((n_pages, T, H, D), generator=gen, device="cuda").to(torch.bfloat16)
+    q = torch.randn((S * L, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    cu = torch.arange(0, S * L + 1, L, dtype=torch.int32, device="cuda")
+    kl = torch.full((S,), L, dtype=torch.int32, device="cuda")
+    scale = D ** -0.5
+
+    def run():
+        flash_attn_varlen_func(q=q, k=wk, v=wv, out=out, cu_seqlens_q=cu, max_seqlen_q=L, seqused_k=kl,
+                               max_seqlen_k=L, softmax_scale=scale, causal=True, block_table=bt)
+
+    run()
+    torch.cuda.synchronize()
+    # fp32 reference on sampled query rows of sequence 0
+    rows = torch.from_numpy(np.sort(rng.choice(L, size=min(L, 48), replace=False))).cuda()
+    pg = bt[0].long()
+    k0 = wk[pg].reshape(-1, H, D)[:L].float().repeat_interleave(G, dim=1)  # [L, Hq, D]
+    v0 = wv[pg].reshape(-1, H, D)[:L].float().repeat_interleave(G, dim=1)
+    s = torch.einsum("rhd,khd->hrk", q[rows].float(), k0) * scale
+    s = s.masked_fill(torch.arange(L, device="cuda")[None, None, :] > rows[None, :, None], float("-inf"))
+    ref = torch.einsum("hrk,khd->rhd", torch.softmax(s, -1), v0)
+    err = (out[rows].float() - ref).abs()
+    valid = bool(torch.isfinite(out.float()).all() and (err <= 2e-2 + 1e-2 * ref.abs()).all())
+    for _ in range(2):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(1, args.prefill_reps)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    flops = 4.0 * D * H * G * S * (L * (L + 1) / 2)
+    log(f"prefill {S}x{L} Hq{H * G}/H{H}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s, sampled max err "
+        f"{err.max().item():.3e}, valid {valid}")
+    return dict(ms=ms, flops=flops, valid=valid, max_err=err.max().item())
+
+
 def encode_bench(torch, args) -> dict:
     """Store encode kernel over BASELINE config 3's shape: ``--encode-blocks``
     completed blocks x 8 KV heads x K/V, 10% Student-t(2) x 16 values, an
@@ -343,6 +398,10 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-encode", action="store_true")
     ap.add_argument("--no-raw-arm", action="store_true", help="skip the all-raw (BF16 paged) comparison arm")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-seqs", type=int, default=4)
+    ap.add_argument("--prefill-len", type=int, default=8192)
+    ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3x (scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -366,6 +425,7 @@ def main() -> None:
     torch.cuda.set_device(int(os.environ.get("LOCAL_RANK", "0")))
     res = decode_bench(torch, args)
     enc = None if args.no_encode else encode_bench(torch, args)
+    pre = None if args.no_prefill else prefill_bench(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(torch, res, args)
     raw = None
     if not args.no_raw_arm:
@@ -407,6 +467,13 @@ def main() -> None:
                      "algo_bytes_per_launch": res["algo_bytes"]},
         "cpu_baseline": cpu,
     }
+    if pre is not None:
+        tf = pre["flops"] / (pre["ms"] / 1e3) / 1e12
+        line["prefill"] = {"workload": f"config 4 prefill: {args.prefill_seqs} x {args.prefill_len} causal, Hq 32 / "
+                                       "H 8 (GQA 4), paged BF16 workspace", "ms": round(pre["ms"], 3),
+                           "tflops": round(tf, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                           "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "validated": pre["valid"],
+                           "sampled_max_abs_err": pre["max_err"]}
     if raw is not None:
         line["bf16_paged_arm"] = {
             "what": "same step over all-raw records (every record 32 KB BF16: the paged BF16 baseline)",
