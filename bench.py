@@ -298,7 +298,7 @@ def encode_bench(torch, args) -> dict:
     chunk = 2048 * T
     for t0 in range(0, n * T, chunk):
         t1 = min(n * T, t0 + chunk)
-        kv = gen_kv(torch, gen, t1 - t0, H, scales_t, heavy=0.1)
+        kv = gen_kv(torch, gen, t1 - t0, H, scales_t, heavy=args.encode_heavy)
         store.write(0, kv[0], kv[1], slots[t0:t1])
         del kv
     torch.cuda.synchronize()
@@ -394,6 +394,7 @@ def main() -> None:
     ap.add_argument("--units", type=int, default=0, help="override decode_units()")
     ap.add_argument("--encode-blocks", type=int, default=32768)
     ap.add_argument("--encode-reps", type=int, default=3)
+    ap.add_argument("--encode-heavy", type=float, default=0.1, help="Student-t(2) x 16 share of encode values")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-encode", action="store_true")

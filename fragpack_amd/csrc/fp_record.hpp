@@ -103,6 +103,17 @@ __device__ __forceinline__ int wave_sum(int v) {
 // Orders this wave's earlier LDS writes before its later LDS reads made by
 // other lanes (DS instructions of one wave complete in order; this only
 // stops the compiler from moving accesses across it).
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS (and
+// scalar) operations, not for its global loads / stores, so prefetches stay
+// in flight across it.  Use only where no global memory written before the
+// barrier is read by another wave after it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();

@@ -9,6 +9,8 @@
 // side and the tests read them; the encoder produces the reference codec's
 // exact bytes (fragpack/compression/attn_page.py:146-209).
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 #include "../../include/fragpack_hip.h"
@@ -36,6 +38,7 @@ enum : int { kTagLive = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
 
 constexpr int kPrepThreads = 1024;
 constexpr int kThreads = 256;
+constexpr int kEncodeWgPerCu = 3;  // resident encode workgroups per CU (VGPR-bound; LDS stage 32 KB each)
 
 struct Store {
   int32_t* counters;
@@ -95,16 +98,39 @@ __device__ __forceinline__ uint8_t* staging_addr(const Store& s, int w, int laye
 }
 
 // Overflow slot allocator over a bitmap (set = in use), safe against a
-// concurrent allocator on another stream.  Returns -1 when full.
-__device__ int ovf_alloc(const Store& s, uint32_t hint) {
-  for (int i = 0; i < s.ovf_words; ++i) {
-    const int w = (int)((hint + (uint32_t)i) % (uint32_t)s.ovf_words);
-    uint32_t cur = __hip_atomic_load(&s.ovf_bits[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    while (cur != 0xffffffffu) {
-      const int bit = __builtin_ctz(~cur);
-      const uint32_t prev = atomicOr(&s.ovf_bits[w], 1u << bit);
-      if (!(prev & (1u << bit))) return 32 * w + bit;
-      cur = prev | (1u << bit);
+// concurrent allocator on another stream.  Returns -1 when full.  Called by
+// one whole wavefront: 64 bitmap words are read per round (in scan order from
+// the hint word, like the reference's serial probe, hbm_kv.cu:89-101) and the
+// earliest word with a free bit is claimed by atomicOr, so a full pool costs
+// ovf_words / 64 load rounds rather than ovf_words dependent loads.
+__device__ int ovf_alloc_wave(const Store& s, uint32_t hint, int lane) {
+  const uint32_t nw = (uint32_t)s.ovf_words;
+  for (uint32_t base = 0; base < nw; base += 64) {
+    const uint32_t i = base + (uint32_t)lane;
+    int w = -1;
+    uint32_t cur = 0xffffffffu;
+    if (i < nw) {
+      w = (int)((hint + i) % nw);
+      cur = __hip_atomic_load(&s.ovf_bits[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    uint64_t avail = __ballot(cur != 0xffffffffu);
+    while (avail) {
+      const int src = __builtin_ctzll(avail);
+      int got = -1;
+      if (lane == src) {
+        while (cur != 0xffffffffu) {
+          const int bit = __builtin_ctz(~cur);
+          const uint32_t prev = atomicOr(&s.ovf_bits[w], 1u << bit);
+          if (!(prev & (1u << bit))) {
+            got = 32 * w + bit;
+            break;
+          }
+          cur = prev | (1u << bit);
+        }
+      }
+      got = __shfl(got, src, 64);
+      if (got >= 0) return got;
+      avail &= avail - 1;
     }
   }
   return -1;
@@ -282,10 +308,13 @@ struct EncResult {
 // workgroup.  Leaves the escape/raw exclusive prefixes of this thread in
 // eo / ro.
 __device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared& sh, uint32_t (&sym)[6],
-                                                 uint64_t& emask, uint64_t& rmask, int& eo, int& ro) {
+                                                 uint32_t (&en)[8], uint64_t& emask, uint64_t& rmask, int& eo,
+                                                 int& ro) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 #pragma unroll
   for (int i = 0; i < 6; ++i) sym[i] = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) en[i] = 0;
   emask = 0;
   rmask = 0;
 #pragma unroll
@@ -304,6 +333,9 @@ __device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared
       }
       if (r >= kPrimaryDirect) emask |= 1ull << sc;
       if (r >= kTableEntries) rmask |= 1ull << sc;
+      // escape nibble: extended-table index, or 15 for a raw scalar
+      const uint32_t nib = r < kPrimaryDirect ? 0u : r < kTableEntries ? (uint32_t)(r - kPrimaryDirect) : (uint32_t)kRawNibble;
+      en[st] |= nib << (4 * e);
     }
   }
   const int ne = __popcll(emask), nr = __popcll(rmask);
@@ -317,7 +349,7 @@ __device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared
     sh.wsum[1][2 * wave] = r31;
     sh.wsum[1][2 * wave + 1] = r63 - r31;
   }
-  __syncthreads();
+  lds_barrier();
   int ebase = 0, rbase = 0, etot = 0, rtot = 0, rmax = 0;
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
@@ -342,25 +374,42 @@ __device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared
 
 // Builds the variable region in sh.var32 (coded records only).  Caller
 // zeroed sh.var32 before enc_analyse's barrier.
-__device__ __forceinline__ void enc_var(const uint4 (&wd)[8], EncShared& sh, const EncResult& res, uint64_t emask,
-                                        int eo, int ro) {
-  uint64_t m = emask;
-  while (m) {
-    const int sc = __builtin_ctzll(m);
-    m &= m - 1;
-    const int st = sc >> 3, e = sc & 7;
-    uint4 w = wd[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i)
-      if (st == i) w = wd[i];
-    const uint32_t high = ((u4(w, e >> 1) >> (16 * (e & 1))) >> 8) & 0xffu;
-    const int r = sh.rank[high];
-    const uint32_t nib = r < kTableEntries ? (uint32_t)(r - kPrimaryDirect) : (uint32_t)kRawNibble;
-    const int bit = 8 * kHeaderBytes + 4 * eo;
-    atomicOr(&sh.var32[bit >> 5], nib << (bit & 31));
-    if (r >= kTableEntries) sh.var32[(res.raw_offset >> 2) + ro++] = (uint32_t)eo | (high << 16);
-    ++eo;
-  }
+__device__ __forceinline__ void enc_var(const uint4 (&wd)[8], const uint32_t (&en)[8], EncShared& sh,
+                                        const EncResult& res, uint64_t emask, int eo, int ro) {
+  // Nibbles of this thread's escapes are contiguous in the stream (escape
+  // ordinals eo ..): gather them per 32-bit stream word in a register and
+  // OR each word into LDS once (only words shared with a neighbour thread
+  // need the atomic).  Word st's escapes are visited with static st so the
+  // data words stay in registers; the nibbles come from the analysis.
+  int bitpos = 8 * kHeaderBytes + 4 * eo;
+  int acc_word = bitpos >> 5;
+  uint32_t acc = 0;
+  static_for<0, 8>([&](auto st_c) {
+    constexpr int st = decltype(st_c)::value;
+    uint32_t m = (uint32_t)(emask >> (8 * st)) & 0xFFu;
+    const uint32_t nw = en[st];
+    while (m) {
+      const int e = __builtin_ctz(m);
+      m &= m - 1;
+      const uint32_t nib = (nw >> (4 * e)) & 0xFu;
+      const int word = bitpos >> 5;
+      if (word != acc_word) {
+        if (acc) atomicOr(&sh.var32[acc_word], acc);
+        acc = 0;
+        acc_word = word;
+      }
+      acc |= nib << (bitpos & 31);
+      if (nib == (uint32_t)kRawNibble) {
+        const uint4 wv = wd[st];
+        // high byte of scalar e (bytes 1, 3 of each dword)
+        const uint32_t hb = e < 4 ? perm(wv.y, wv.x, 0x07050301u) : perm(wv.w, wv.z, 0x07050301u);
+        sh.var32[(res.raw_offset >> 2) + ro++] = (uint32_t)eo | (((hb >> (8 * (e & 3))) & 0xffu) << 16);
+      }
+      bitpos += 4;
+      ++eo;
+    }
+  });
+  if (acc) atomicOr(&sh.var32[acc_word], acc);
   if (threadIdx.x == 0) {
     sh.var32[0] = res.etot;
     sh.var32[1] = res.rtot;
@@ -403,83 +452,198 @@ __device__ __forceinline__ void enc_store(uint8_t* dst, const uint4 (&wd)[8], co
     *reinterpret_cast<uint4*>(dst + kDenseBytes + 16 * i) = reinterpret_cast<const uint4*>(sh.var32)[i];
 }
 
-// grid (max_close, 2H): workgroup (i, kvh) encodes record kvh of
-// close_list[i] at ``layer`` from staging into the block's arena page (each
-// record takes the next kDenseBytes + var_len bytes, claimed by CAS on
-// fill), or raw into the overflow pool when it does not code or no longer
-// fits.  Also hands the slot's record to the block's heir (hbm_kv.cu:278-289).
-__global__ void __launch_bounds__(kThreads) encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes,
-                                                         const uint8_t* rank_of) {
+// Persistent encoder: workgroup g encodes records r = g, g + grid, ... of
+// the n_closes * 2H records of this step (record r: kvh = r / n_closes of
+// block close_list[r % n_closes]) from staging into the block's arena page (each record
+// takes the next kDenseBytes + var_len bytes, claimed by CAS on fill), or raw
+// into the overflow pool when it does not code or no longer fits; and hands
+// the slot's record to the block's heir (hbm_kv.cu:262-429).  While record r
+// is encoded from registers, record r + grid streams from HBM straight into
+// this workgroup's LDS stage (global_load_lds: no registers held), each wave
+// loading exactly the 16-byte words its own lanes read back.
+struct EncStage {
+  uint4 w[8][kThreads];  // record words: [st][thread], the staging layout
+};
+
+__device__ __forceinline__ void stage_record(EncStage& st_buf, const uint8_t* src) {
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  typedef const void __attribute__((address_space(1)))* gptr_t;
+  typedef void __attribute__((address_space(3)))* lptr_t;
+#pragma unroll
+  for (int st = 0; st < 8; ++st)
+    __builtin_amdgcn_global_load_lds((gptr_t)(src + 16 * (256 * st + tid)), (lptr_t)&st_buf.w[st][64 * wave], 16, 0,
+                                     0);
+}
+
+// Record r of the step: block close_list[r % n_closes], record r / n_closes
+// of it -- consecutive records (running at the same time) belong to
+// different blocks, so their fill-counter CAS rarely collide.
+__device__ __forceinline__ const uint8_t* record_src(const Store& s, int layer, int r, int n_closes) {
+  const int b = s.close_list[r % n_closes];
+  return staging_addr(s, s.wslot[b], layer, r / n_closes);
+}
+
+#ifdef FP_TRACE_ENC
+__device__ uint64_t fp_enc_trace[1024 * 16];
+#define ENC_STAMP(k)                                                              \
+  do {                                                                            \
+    if (threadIdx.x == 0 && blockIdx.x < 1024 && r < 64 * (int)gridDim.x)       \
+      fp_enc_trace[blockIdx.x * 16 + (k)] += __builtin_amdgcn_s_memrealtime();   \
+  } while (0)
+#else
+#define ENC_STAMP(k) \
+  do {               \
+  } while (0)
+#endif
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kEncodeWgPerCu)))
+encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint8_t* rank_of) {
   __shared__ EncShared sh;
-  if ((int)blockIdx.x >= s.counters[kCloses]) return;
-  const int kvh = blockIdx.y, tid = threadIdx.x;
-  const int b = s.close_list[blockIdx.x];
-  uint8_t* src = staging_addr(s, s.wslot[b], layer, kvh);
-  const int64_t idx = ((int64_t)layer * s.NB + b) * 2 * s.H + kvh;
-  sh.rank[tid] = rank_of[((int64_t)layer * 2 * s.H + kvh) * 256 + tid];
-  for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
-  uint4 wd[8];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) wd[st] = ld16(src + 16 * (256 * st + tid));
-  const int heir = s.close_list[s.cap + blockIdx.x];
-  if (heir >= 0) {
-    const uint8_t* from = staging_addr(s, s.wslot[heir], layer, kvh);
-#pragma unroll
-    for (int st = 0; st < 8; ++st)
-      *reinterpret_cast<uint4*>(src + 16 * (256 * st + tid)) = ld16(from + 16 * (256 * st + tid));
-    if (tid == 0) s.rec_addr[((int64_t)layer * s.NB + heir) * 2 * s.H + kvh] = reinterpret_cast<int64_t>(src);
+  __shared__ EncStage stage;
+  const int tid = threadIdx.x;
+  const int per = 2 * s.H;
+  const int n_closes = s.counters[kCloses];
+  const int n_rec = n_closes * per;
+  int r = blockIdx.x;
+  if (r >= n_rec) return;
+  // Record metadata runs ahead of the data: at record r the stage streams
+  // record r + grid (address known since the previous record), the slot of
+  // r + 2 grid is read and the close entry of r + 3 grid.
+  const int g = (int)gridDim.x;
+  int b = s.close_list[r % n_closes];
+  int heir = s.close_list[s.cap + r % n_closes];
+  uint8_t* src = staging_addr(s, s.wslot[b], layer, r / n_closes);
+  stage_record(stage, src);
+  int b1 = 0, heir1 = -1, w1 = 0, b2 = 0, heir2 = -1;
+  if (r + g < n_rec) {
+    b1 = s.close_list[(r + g) % n_closes];
+    heir1 = s.close_list[s.cap + (r + g) % n_closes];
+    w1 = s.wslot[b1];
   }
-  __syncthreads();
-  uint32_t sym[6];
-  uint64_t emask, rmask;
-  int eo, ro;
-  const EncResult res = enc_analyse(wd, sh, sym, emask, rmask, eo, ro);
-  if (tid == 0) {
-    int off = -1;
+  if (r + 2 * g < n_rec) {
+    b2 = s.close_list[(r + 2 * g) % n_closes];
+    heir2 = s.close_list[s.cap + (r + 2 * g) % n_closes];
+  }
+  int rank_kvh = -1;
+  for (; r < n_rec; r += g) {
+    const int kvh = r / n_closes;
+    ENC_STAMP(0);
+    const int64_t idx = ((int64_t)layer * s.NB + b) * per + kvh;
+    int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
+    if (kvh != rank_kvh) {  // consecutive records mostly share (layer, kvh)
+      sh.rank[tid] = rank_of[((int64_t)layer * per + kvh) * 256 + tid];
+      rank_kvh = kvh;
+    }
+    for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
+    // the fill value is only a first guess for the claim: fetch it early
+    int cur = 0;
+    if (tid == 0) cur = __hip_atomic_load(fill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // this record's words: the wave's own LDS loads, then into registers
+    __builtin_amdgcn_s_waitcnt(0);
+    uint4 wd[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) wd[st] = stage.w[st][tid];
+    __builtin_amdgcn_s_waitcnt(0);  // reads done before the stage is refilled
+    ENC_STAMP(1);
+    uint8_t* src1 = src;
+    if (r + g < n_rec) {
+      src1 = staging_addr(s, w1, layer, (r + g) / n_closes);
+      stage_record(stage, src1);
+    }
+    int w2 = 0, b3 = 0, heir3 = -1;
+    if (r + 2 * g < n_rec) w2 = s.wslot[b2];
+    if (r + 3 * g < n_rec) {
+      b3 = s.close_list[(r + 3 * g) % n_closes];
+      heir3 = s.close_list[s.cap + (r + 3 * g) % n_closes];
+    }
+    if (heir >= 0) {
+      const uint8_t* from = staging_addr(s, s.wslot[heir], layer, kvh);
+#pragma unroll
+      for (int st = 0; st < 8; ++st)
+        *reinterpret_cast<uint4*>(src + 16 * (256 * st + tid)) = ld16(from + 16 * (256 * st + tid));
+      if (tid == 0) s.rec_addr[((int64_t)layer * s.NB + heir) * per + kvh] = reinterpret_cast<int64_t>(src);
+    }
+    lds_barrier();
+    ENC_STAMP(2);
+    uint32_t sym[6];
+    uint64_t emask, rmask;
+    int eo, ro;
+    uint32_t en[8];
+    const EncResult res = enc_analyse(wd, sh, sym, en, emask, rmask, eo, ro);
+    ENC_STAMP(3);
     if (res.codes) {
-      int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
+      // first claim attempt in flight while the variable region is built
       const int need = kDenseBytes + res.var_len;
-      int cur = __hip_atomic_load(fill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      while (cur + need <= page_bytes) {
-        const int prev = atomicCAS(fill, cur, cur + need);
-        if (prev == cur) {
-          off = cur;
-          break;
+      int prev = -1;
+      if (tid == 0 && cur + need <= page_bytes) prev = atomicCAS(fill, cur, cur + need);
+      enc_var(wd, en, sh, res, emask, eo, ro);
+      ENC_STAMP(4);
+      if (tid == 0) {
+        int off = -1;
+        if (cur + need <= page_bytes) {
+          if (prev == cur) {
+            off = cur;
+          } else {
+            cur = prev;
+            while (cur + need <= page_bytes) {
+              prev = atomicCAS(fill, cur, cur + need);
+              if (prev == cur) {
+                off = cur;
+                break;
+              }
+              cur = prev;
+            }
+          }
         }
-        cur = prev;
+        if (off < 0) atomicAdd(&s.counters[kSpills], 1);
+        sh.s_off = off;
       }
-      if (off < 0) atomicAdd(&s.counters[kSpills], 1);
+    } else if (tid == 0) {
+      sh.s_off = -1;
     }
-    sh.s_off = off;
-  }
-  __syncthreads();
-  if (sh.s_off < 0) {
-    if (tid == 0) {
-      const int slot = ovf_alloc(s, (uint32_t)(b * 2 * s.H + kvh));
-      if (slot < 0) atomicAdd(&s.counters[kErrOverflow], 1);
-      atomicAdd(&s.counters[kFallbacks], 1);
-      atomicAdd(&s.counters[kEncoded], 1);
-      sh.s_ovf = slot;
-    }
-    __syncthreads();
-    if (sh.s_ovf < 0) return;  // record stays in staging (data loss is counted)
-    uint8_t* dst = s.ovf_base + (int64_t)sh.s_ovf * kRawRecord;
+    lds_barrier();
+    ENC_STAMP(5);
+    if (sh.s_off < 0) {
+      if (tid < 64) {
+        const int slot = ovf_alloc_wave(s, (uint32_t)(b * per + kvh), tid);
+        if (tid == 0) {
+          if (slot < 0) atomicAdd(&s.counters[kErrOverflow], 1);
+          atomicAdd(&s.counters[kFallbacks], 1);
+          atomicAdd(&s.counters[kEncoded], 1);
+          sh.s_ovf = slot;
+        }
+      }
+      lds_barrier();
+      const int slot = sh.s_ovf;
+      if (slot >= 0) {  // else the record stays in staging (data loss is counted)
+        uint8_t* dst = s.ovf_base + (int64_t)slot * kRawRecord;
 #pragma unroll
-    for (int st = 0; st < 8; ++st) *reinterpret_cast<uint4*>(dst + 16 * (256 * st + tid)) = wd[st];
-    if (tid == 0) {
-      s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
-      s.rec_len[idx] = kRawVarLen;
+        for (int st = 0; st < 8; ++st) *reinterpret_cast<uint4*>(dst + 16 * (256 * st + tid)) = wd[st];
+        if (tid == 0) {
+          s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
+          s.rec_len[idx] = kRawVarLen;
+        }
+      }
+    } else {
+      uint8_t* dst = arena + (int64_t)b * page_bytes + sh.s_off;
+      enc_store(dst, wd, sym, sh, res.var_len);
+      if (tid == 0) {
+        s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
+        s.rec_len[idx] = res.var_len;
+        atomicAdd(&s.counters[kEncoded], 1);
+      }
     }
-    return;
-  }
-  enc_var(wd, sh, res, emask, eo, ro);
-  __syncthreads();
-  uint8_t* dst = arena + (int64_t)b * page_bytes + sh.s_off;
-  enc_store(dst, wd, sym, sh, res.var_len);
-  if (tid == 0) {
-    s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
-    s.rec_len[idx] = res.var_len;
-    atomicAdd(&s.counters[kEncoded], 1);
+    ENC_STAMP(6);
+    lds_barrier();  // sh (var32, s_off, s_ovf; rank on a head change) is reused by the next record
+    ENC_STAMP(7);
+    b = b1;
+    heir = heir1;
+    src = src1;
+    b1 = b2;
+    heir1 = heir2;
+    w1 = w2;
+    b2 = b3;
+    heir2 = heir3;
   }
 }
 
@@ -624,7 +788,8 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
   uint32_t sym[6];
   uint64_t emask, rmask;
   int eo, ro;
-  const EncResult res = enc_analyse(wd, sh, sym, emask, rmask, eo, ro);
+  uint32_t en[8];
+  const EncResult res = enc_analyse(wd, sh, sym, en, emask, rmask, eo, ro);
   uint8_t* dst = out + (int64_t)i * kRawRecord;
   if (!res.codes) {
 #pragma unroll
@@ -632,7 +797,7 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
     if (tid == 0) lens[i] = kRawRecord;
     return;
   }
-  enc_var(wd, sh, res, emask, eo, ro);
+  enc_var(wd, en, sh, res, emask, eo, ro);
   __syncthreads();
   enc_store(dst, wd, sym, sh, res.var_len);
   if (tid == 0) lens[i] = kDenseBytes + res.var_len;
@@ -755,7 +920,7 @@ __global__ void __launch_bounds__(kThreads) blob_import_kernel(Store s, const ui
     return;
   }
   const int32_t* lens = table + l * per;
-  if (tid == 0) {
+  if (tid < 64) {  // wave 0: every lane runs the same placement, the allocator uses the wave
     const int64_t page = arena_stride[l];
     const int64_t page_ptr = arena_base[l] + (int64_t)b * page;
     int64_t from = head + before;
@@ -767,20 +932,24 @@ __global__ void __launch_bounds__(kThreads) blob_import_kernel(Store s, const ui
         d = page_ptr + fill;
         fill += n;
       } else {
-        const int slot = ovf_alloc(s, (uint32_t)(b * per + placed));
+        const int slot = ovf_alloc_wave(s, (uint32_t)(b * per + placed), tid);
         if (slot < 0) break;
         d = reinterpret_cast<int64_t>(s.ovf_base) + (int64_t)slot * kRawRecord;
       }
-      s_src[placed] = from;
-      s_dst[placed] = d;
+      if (tid == 0) {
+        s_src[placed] = from;
+        s_dst[placed] = d;
+      }
       from += n;
     }
-    s_fail = placed < per;
-    if (s_fail) {
-      for (int k = 0; k < placed; ++k) ovf_free(s, s_dst[k]);
-      atomicOr(&status[i], kBlobNoOverflow);
-    } else {
-      s.fill[(int64_t)l * s.NB + b] = fill;
+    if (tid == 0) {
+      s_fail = placed < per;
+      if (s_fail) {
+        for (int k = 0; k < placed; ++k) ovf_free(s, s_dst[k]);
+        atomicOr(&status[i], kBlobNoOverflow);
+      } else {
+        s.fill[(int64_t)l * s.NB + b] = fill;
+      }
     }
   }
   __syncthreads();
@@ -837,6 +1006,12 @@ extern "C" int fp_hbm_write(const fp_store_t* d, const void* key, int64_t k_s0, 
   return 0;
 }
 
+#ifdef FP_TRACE_ENC
+extern "C" int fp_enc_trace_read(uint64_t* host, int64_t n) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(fp_enc_trace), n * sizeof(uint64_t)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 extern "C" int fp_hbm_encode(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
                              int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream) {
   if (max_close == 0) return 0;
@@ -847,8 +1022,19 @@ extern "C" int fp_hbm_encode(const fp_store_t* d, const uint8_t* rank_of, int64_
   FP_CHECK(layer >= 0 && layer < d->num_layers && arena % 16 == 0, "bad layer or arena address");
   FP_CHECK(max_close < (1LL << 31), "too many closing blocks");
   const Store s = make_store(d);
-  hipLaunchKernelGGL(encode_kernel, dim3((unsigned)max_close, (unsigned)(2 * d->kv_heads)), dim3(kThreads), 0,
-                     stream, s, (int)layer, reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+  // persistent grid: a few workgroups per CU, capped by the records there can be
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    FP_CHECK(hipGetDevice(&dev) == hipSuccess &&
+                 hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0,
+             "cannot query the CU count");
+    cus = n;
+  }
+  const int64_t records = max_close * 2 * d->kv_heads;
+  const int64_t grid = std::min<int64_t>(records, (int64_t)cus * kEncodeWgPerCu);
+  hipLaunchKernelGGL(encode_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
+                     reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
   FP_LAUNCH_CHECK();
   return 0;
 }
