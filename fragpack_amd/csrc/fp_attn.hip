@@ -28,6 +28,8 @@
 // * Split-KV partials are merged in the same kernel: the last workgroup to
 //   finish a (sequence, head) merges all its chunks.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <math.h>
 #include <stdint.h>
 
@@ -42,10 +44,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 
+#ifndef FP_DECODE_BATCHED
+#define FP_DECODE_BATCHED 1
+#endif
+#ifndef FP_PERSIST
+#define FP_PERSIST 1
+#endif
 #ifndef FP_ATTN_WAVES_PER_EU
 #define FP_ATTN_WAVES_PER_EU 3  // occupancy target of attn_kernel (VGPR budget 512 / 3)
 #endif
 constexpr int kWaves = 4;          // wavefronts per workgroup = slabs per record
+constexpr int kAttnPerCu = FP_ATTN_WAVES_PER_EU;  // resident workgroups per CU (kWaves = SIMDs per CU)
 constexpr float kLazyMax = 8.f;    // log2 headroom of the speculative softmax reference
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
 
@@ -70,7 +79,7 @@ struct AttnParams {
   float scale_log2;
 };
 
-// Plan layout (int32): [0] ppc, [1] budget, [2, 2 + 2 units) (sequence, first
+// Plan layout (int32): [0] ppc, [1] units in use, [2, 2 + 2 units) (sequence, first
 // page) per unit (sequence -1: idle), [2 + 2 units, 2 + 4 units) (first
 // unit, chunks) per sequence -- the reference's layout --, then at
 // ud_offset(units) 8 ints per unit (sequence, first page, pages, context,
@@ -104,18 +113,27 @@ __device__ __forceinline__ int wave_total(int x) {
   return __builtin_amdgcn_readlane(wave_scan_dpp<kMax>(x), 63);
 }
 
-// Work plan.  Same policy and layout as the reference planner
-// (fused_attn_decode.cu:48-163): every sequence is cut into chunks of ``ppc``
-// pages, ``ppc`` the smallest for which the live rows fit ``budget`` units.
-// Wave 0 runs the search with the page counts in registers (one DPP
-// reduction per step, division by the uniform ``ppc`` via a reciprocal) and
-// writes each sequence's first unit; then every thread fills the descriptors
-// of its units in parallel, locating the sequence by binary search over the
-// first units (in LDS up to kPlanLds sequences).  The descriptors also carry
-// the first two block ids of each chunk.
+// Work plan (layout of the reference planner, fused_attn_decode.cu:48-163;
+// policy of this build).  Every sequence is cut into chunks of ``ppc``
+// pages.  The reference takes the smallest ``ppc`` whose chunks fit one wave
+// of units; on gfx950 the attention grid is persistent (``slots`` resident
+// workgroups over all KV heads), so ``ppc`` is chosen to minimise the
+// modelled makespan instead:
+//   cost(ppc) = ceil(chunks(ppc) * kvh / slots) * (ppc + kUnitCost)
+// over the candidates ppc = ceil(longest / c), c = 1..kPlanCands, with
+// chunks(ppc) <= units; ties go to the larger ppc.  Each wave scores
+// kPlanCands / 16 candidates with the page counts in registers (one DPP
+// reduction per candidate, division by a reciprocal); wave 0 then writes
+// each sequence's first unit and every thread fills the descriptors of its
+// units, locating the sequence by binary search over the first units (in LDS
+// up to kPlanLds sequences).  The descriptors also carry the first two block
+// ids of each chunk.  plan[1] holds the number of units in use.
 constexpr int kPlanCache = 16;  // page counts of batch <= 64 * 16 kept in registers
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kPlanLds = 8192;
+constexpr int kPlanCands = 64;
+constexpr int kUnitCost = 1;  // fixed cost of a unit (metadata, Q, merge) in pages
 
 struct Divider {  // x / d for 0 <= x < 2^24, 1 <= d
   int d;
@@ -132,59 +150,50 @@ struct Divider {  // x / d for 0 <= x < 2^24, 1 <= d
 
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __restrict__ seq_lens,
                                                             const int32_t* __restrict__ block_table, int64_t bt_stride,
-                                                            int32_t* __restrict__ plan, int batch, int units, int kvh) {
+                                                            int32_t* __restrict__ plan, int batch, int units, int kvh,
+                                                            int slots) {
   __shared__ int firsts[kPlanLds + 1];
-  __shared__ int shared_used, shared_ppc;
+  __shared__ unsigned long long best;
+  __shared__ int shared_used;
   int32_t* seq_plan = plan + 2 + 2 * units;
   const bool lds = batch <= kPlanLds;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    int pg[kPlanCache];
-    int total = 0, longest = 0, active = 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) best = ~0ull;
+  int pg[kPlanCache];
+  int longest = 0;
+  static_for<0, kPlanCache>([&](auto k) {
+    pg[k] = 0;
+    if (64 * k < batch) {
+      const int b = lane + 64 * k;
+      pg[k] = b < batch ? pages_of(seq_lens, b) : 0;
+      longest = max(longest, pg[k]);
+    }
+  });
+  for (int b = lane + 64 * kPlanCache; b < batch; b += 64) longest = max(longest, pages_of(seq_lens, b));
+  longest = wave_total<true>(longest);
+  auto count_chunks = [&](int ppc) {
+    const Divider dv(ppc);
+    int c = 0;
     static_for<0, kPlanCache>([&](auto k) {
-      pg[k] = 0;
-      if (64 * k < batch) {
-        const int b = lane + 64 * k;
-        pg[k] = b < batch ? pages_of(seq_lens, b) : 0;
-        total += pg[k];
-        longest = max(longest, pg[k]);
-        active += pg[k] > 0;
-      }
+      if (64 * k < batch) c += dv.chunks(pg[k]);
     });
-    for (int b = lane + 64 * kPlanCache; b < batch; b += 64) {
-      const int n = pages_of(seq_lens, b);
-      total += n;
-      longest = max(longest, n);
-      active += n > 0;
+    for (int b = lane + 64 * kPlanCache; b < batch; b += 64) c += dv.chunks(pages_of(seq_lens, b));
+    return wave_total<false>(c);
+  };
+  __syncthreads();  // best initialised
+  for (int k = 0; k < kPlanCands / kPlanWaves; ++k) {
+    const int c = wave * (kPlanCands / kPlanWaves) + k + 1;
+    const int ppc = max(1, (longest + c - 1) / c);
+    const int n = count_chunks(ppc);
+    if (n <= units && lane == 0) {
+      const int64_t rounds = ((int64_t)n * kvh + slots - 1) / slots;
+      const uint64_t cost = (uint64_t)(rounds * (ppc + kUnitCost));
+      atomicMin(&best, (cost << 24) | (uint64_t)(0xFFFFFF - ppc));
     }
-    total = wave_total<false>(total);
-    longest = wave_total<true>(longest);
-    active = wave_total<false>(active);
-    auto count_chunks = [&](int ppc) {
-      const Divider dv(ppc);
-      int c = 0;
-      static_for<0, kPlanCache>([&](auto k) {
-        if (64 * k < batch) c += dv.chunks(pg[k]);
-      });
-      for (int b = lane + 64 * kPlanCache; b < batch; b += 64) c += dv.chunks(pages_of(seq_lens, b));
-      return wave_total<false>(c);
-    };
-    const int capacity = max(1, units - batch + active);
-    const int wave = units - batch + 1;
-    int budget = min(capacity, max(active, wave));
-    if (capacity > budget) {
-      const int tail_bound = 2 * max(1, (total + budget - 1) / budget);
-      if (count_chunks(tail_bound) > budget) budget = capacity;
-    }
-    int lo = max(1, (total + budget - 1) / budget), hi = max(1, longest);
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (count_chunks(mid) <= budget)
-        hi = mid;
-      else
-        lo = mid + 1;
-    }
-    const int ppc = lo;
+  }
+  __syncthreads();
+  const int ppc = 0xFFFFFF - (int)(best & 0xFFFFFFu);
+  if (wave == 0) {
     const Divider dv(ppc);
     int used = 0;
     auto place = [&](int b, int n) {
@@ -208,13 +217,12 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __res
     if (lane == 0) {
       if (lds) firsts[batch] = used;
       shared_used = used;
-      shared_ppc = ppc;
       plan[0] = ppc;
-      plan[1] = budget;
+      plan[1] = used;
     }
   }
   __syncthreads();
-  const int used = shared_used, ppc = shared_ppc;
+  const int used = shared_used;
   const int ud0 = ud_offset(units);
   auto first_of = [&](int b) { return b == batch ? used : lds ? firsts[b] : seq_plan[2 * b]; };
   for (int u = threadIdx.x; u < units; u += kPlanThreads) {
@@ -243,8 +251,8 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __res
     ud[0] = make_int4(b, p0, np, seq);
     ud[1] = make_int4(first, c, bt[p0], np > 1 ? bt[p0 + 1] : 0);
   }
-  // merge-group counters of the fused merge; the last arrival of a group
-  // resets its counter, so zeroing is needed only here
+  // merge counters of the fused merge; the last arrival of a (sequence,
+  // head) resets its counter, so zeroing is needed only here
   for (int x = threadIdx.x; x < units * kvh; x += kPlanThreads) plan[ud0 + 8 * units + x] = 0;
 }
 
@@ -313,11 +321,15 @@ struct PageMeta {
   int klen, vlen;
 };
 
-__device__ __forceinline__ PageMeta load_meta(const AttnParams& p, const int32_t* bt, int base, int npages, int h,
-                                              int lane) {
+// Block id of page base + lane of the unit (-1 past its pages).
+__device__ __forceinline__ int load_block(const int32_t* bt, int base, int npages, int lane) {
+  return base + lane < npages ? bt[base + lane] : -1;
+}
+
+__device__ __forceinline__ PageMeta load_meta(const AttnParams& p, int blk, int h) {
   PageMeta m{0u, 0u, 0u, 0u, kRawVarLen, kRawVarLen};
-  if (base + lane < npages) {
-    const int64_t kidx = ((int64_t)bt[base + lane] * 2) * p.kvh + h;
+  if (blk >= 0) {
+    const int64_t kidx = ((int64_t)blk * 2) * p.kvh + h;
     const uint64_t ka = (uint64_t)p.rec_addr[kidx], va = (uint64_t)p.rec_addr[kidx + p.kvh];
     m.klo = (uint32_t)ka;
     m.khi = (uint32_t)(ka >> 32);
@@ -396,18 +408,29 @@ __device__ __forceinline__ int natural_prefix(int cnt, NatPerm np) {
   return __builtin_amdgcn_ds_bpermute(np.from_nat, incl) - cnt;
 }
 
+// Fragment tile [head 8][a 4][c 4] x 16 B: lane (c, n) reads its 8 BF16 of
+// k-chunk a at ((n * 4 + a) * 4 + c) * 16.  Used for Q (dims) and P (tokens).
+__device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, int c) {
+  return *reinterpret_cast<const uint4*>(tile + (((n & 7) * 4 + a) * 4 + c) * 16);
+}
+
 // Decodes this lane's kernel-order thread ``nt`` of the wave's slab ``w`` of
 // record ``r`` (escapes staged in ``esc``, header in ``hdr``) and calls
-// pair(a, word 2a, word 2a + 1) for a = 0..3.
+// pair(a, word 2a, word 2a + 1, fragment a of ``tile``) for a = 0..3.  The
+// four B fragments are read from ``tile`` in the same LDS batch as the
+// escape windows.
 template <typename Pair>
 __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int w, int nt, NatPerm np,
                                             const HeadLut& lut, const uint8_t* esc, const uint32_t* hdr,
-                                            Pair&& pair) {
+                                            const uint8_t* tile, int n, int c, Pair&& pair) {
+  uint4 fr[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) fr[a] = tile_frag(tile, n, a, c);
   uint4 prev;
   auto emit = [&](auto st_c, const uint4& wd) {
     constexpr int st = decltype(st_c)::value;
     if constexpr (st & 1)
-      pair(std::integral_constant<int, (st >> 1)>{}, prev, wd);
+      pair(std::integral_constant<int, (st >> 1)>{}, prev, wd, fr[st >> 1]);
     else
       prev = wd;
   };
@@ -417,13 +440,11 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
   }
   const int e0 = (int)(hdr[4 + w] & 0xFFFFu);  // esc_prefix[2 w]
   const int excl = natural_prefix(thread_escapes(b), np);
+#if FP_DECODE_BATCHED
+  decode_words_batched(b, esc, e0 + excl, lut.p0, lut.p1, emit);
+#else
   decode_words(b, esc, e0 + excl, lut.p0, lut.p1, emit);
-}
-
-// Fragment tile [head 8][a 4][c 4] x 16 B: lane (c, n) reads its 8 BF16 of
-// k-chunk a at ((n * 4 + a) * 4 + c) * 16.  Used for Q (dims) and P (tokens).
-__device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, int c) {
-  return *reinterpret_cast<const uint4*>(tile + (((n & 7) * 4 + a) * 4 + c) * 16);
+#endif
 }
 
 // Optional per-workgroup timeline (built only with -DFP_TRACE): slot k of
@@ -451,39 +472,59 @@ struct AttnShared {
   int last;
 };
 
-// Merges ``count`` (<= 8) split-KV partials of (b, h) -- partial rows
-// ``first_row + k * stride`` (k < count) of opart / ml -- with the
-// online-softmax merge in the log2 domain (the reference's combine,
-// fused_attn_decode.cu:407-425).  ``final``: writes the group's BF16 output
-// rows; else writes the merged partial over item 0.  Whole workgroup:
-// thread t covers row t >> 5, dims 4 (t & 31) .. + 3; every load of the
-// group is issued before any is used.
-__device__ __forceinline__ void merge_group(const AttnParams& p, int b, int h, int64_t first_row, int stride,
-                                            int count, bool final) {
+// Split-KV merge of (b, h) after this workgroup wrote the partial of one of
+// its ``chunks`` units (``first`` .. ``first + chunks - 1``): the last
+// workgroup to arrive merges all of them with the online-softmax merge in the
+// log2 domain (the reference's combine, fused_attn_decode.cu:407-425) and
+// writes the BF16 output rows.  One level: partials are read in batches of
+// kMergeBatch with every load of a batch issued before any is used.  Thread t
+// covers row t >> 5 (query head), dims 4 (t & 31) .. + 3.  The counter
+// p.done[h * units + first] is left at zero.
+constexpr int kMergeBatch = 16;
+__device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh, int b, int h, int first, int chunks) {
+  wait_stores();  // this workgroup's partial is at the coherence point
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t* cnt = p.done + (int64_t)h * p.units + first;
+    const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == chunks - 1;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.last = last;
+  }
+  __syncthreads();
+  if (!sh.last) return;
   const int t = threadIdx.x, g = t >> 5, d = 4 * (t & 31);
   if (g >= p.group) return;
   const rsrc_t ro = coh_rsrc(p.opart), rm = coh_rsrc(p.ml);
-  float2 ms[8];
-  float4 o[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if (k < count) {
-      const int64_t r = (first_row + (int64_t)k * stride) * 8 + g;
-      ms[k] = ld_coh2(rm, r * 2);
-      o[k] = ld_coh4(ro, r * kDim + d);
-    }
-  }
-  float gm = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    if (k < count) gm = fmaxf(gm, ms[k].x);
-  float l = 0.f;
+  const int64_t row0 = ((int64_t)h * p.units + first) * 8 + g;
+  float gm = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (gm != -INFINITY) {
+  for (int k0 = 0; k0 < chunks; k0 += kMergeBatch) {
+    float2 ms[kMergeBatch];
+    float4 o[kMergeBatch];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (k < count) {
-        const float w = __builtin_amdgcn_exp2f(ms[k].x - gm);
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (k0 + k < chunks) {
+        const int64_t r = row0 + (int64_t)(k0 + k) * 8;
+        ms[k] = ld_coh2(rm, r * 2);
+        o[k] = ld_coh4(ro, r * kDim + d);
+      }
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k)
+      if (k0 + k < chunks) bm = fmaxf(bm, ms[k].x);
+    const float nm = fmaxf(gm, bm);
+    if (nm == -INFINITY) continue;
+    const float alpha = __builtin_amdgcn_exp2f(gm - nm);
+    l *= alpha;
+    acc.x *= alpha;
+    acc.y *= alpha;
+    acc.z *= alpha;
+    acc.w *= alpha;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (k0 + k < chunks) {
+        const float w = __builtin_amdgcn_exp2f(ms[k].x - nm);
         l += w * ms[k].y;
         acc.x += w * o[k].x;
         acc.y += w * o[k].y;
@@ -491,55 +532,15 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int b, int h, i
         acc.w += w * o[k].w;
       }
     }
+    gm = nm;
   }
-  if (final) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.x * inv)) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.y * inv)) << 16);
-    const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.z * inv)) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.w * inv)) << 16);
-    *reinterpret_cast<uint2*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + g) * kDim + d) =
-        make_uint2(lo, hi);
-  } else {
-    const int64_t r = first_row * 8 + g;
-    st_coh4(ro, r * kDim + d, acc.x, acc.y, acc.z, acc.w);
-    if ((t & 31) == 0) st_coh2(rm, r * 2, gm, l);
-  }
-}
-
-// Hierarchical merge of (b, h)'s ``chunks`` partials after this workgroup
-// wrote chunk ``s``'s.  Items are merged in groups of 8; the last workgroup
-// to finish a group merges it in place over the group's first item, and the
-// last group of the top level writes the output.  Counters live in
-// p.done[h * units + unit slot] and are left at zero.
-__device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh, int b, int h, int first, int chunks,
-                                             int s) {
-  // chunks >= 2: a single chunk writes its output directly
-  int n_items = chunks, stride = 1;
-  for (int level = 0;; ++level) {
-    const int item = s / stride;
-    const int gfirst = item & ~7;
-    const int gcount = min(8, n_items - gfirst);
-    const bool final = n_items <= 8;
-    if (gcount > 1) {
-      wait_stores();  // this workgroup's partial is at the coherence point
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        int32_t* cnt = p.done + (int64_t)h * p.units + first + gfirst * stride + level;
-        const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gcount - 1;
-        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh.last = last;
-      }
-      __syncthreads();
-      if (!sh.last) return;
-      merge_group(p, b, h, (int64_t)h * p.units + first + (int64_t)gfirst * stride, stride, gcount, final);
-    }
-    // gcount == 1 (never final): the item moves up a level in place
-    if (final) return;
-    s = gfirst * stride;
-    stride *= 8;
-    n_items = (n_items + 7) >> 3;
-  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.x * inv)) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.y * inv)) << 16);
+  const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.z * inv)) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.w * inv)) << 16);
+  *reinterpret_cast<uint2*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + g) * kDim + d) =
+      make_uint2(lo, hi);
 }
 
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FP_ATTN_WAVES_PER_EU))) attn_kernel(AttnParams p) {
@@ -551,53 +552,72 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const int nt = 32 * hh + 4 * g + c;
   const NatPerm np{4 * lane_of_natural(lane), 4 * nt};
   const int n = lane & 15;  // MFMA column = query head within the group
-  const int budget = uniform(p.plan[1]);
+  const int used = uniform(p.plan[1]);  // units in use
   const HeadLut klut = load_lut(p.plut, p.slut, h);
   const HeadLut vlut = load_lut(p.plut, p.slut, p.kvh + h);
 
   FP_STAMP(0);
-  for (int unit = blockIdx.x; unit < budget; unit += gridDim.x) {
-    // unit descriptor: b, first page, pages, context, first unit of b, chunks of b
-    const int32_t* ud = p.plan + p.ud_off + 8 * unit;
-    const int b = uniform(ud[0]);
+  for (int unit = blockIdx.x; unit < used; unit += gridDim.x) {
+    // unit descriptor: b, first page, pages, context, first unit of b,
+    // chunks of b, block of page 0 (both halves loaded together)
+    const int4* udp = reinterpret_cast<const int4*>(p.plan + p.ud_off + 8 * unit);
+    const int4 u0 = udp[0], u1 = udp[1];
+    asm volatile("" ::"v"(u0.x), "v"(u0.y), "v"(u0.z), "v"(u0.w), "v"(u1.x), "v"(u1.y), "v"(u1.z));  // one hop
+    const int b = uniform(u0.x);
     if (b < 0) continue;
-    const int p0 = uniform(ud[1]), npages = uniform(ud[2]), seq = uniform(ud[3]);
-    const int first = uniform(ud[4]), chunks = uniform(ud[5]), blk0 = uniform(ud[6]);
+    const int p0 = uniform(u0.y), npages = uniform(u0.z), seq = uniform(u0.w);
+    const int first = uniform(u1.x), chunks = uniform(u1.y), blk0 = uniform(u1.z);
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
-    // page 0's records straight from the descriptor's block id (one hop
-    // shorter than through the block table); the rest through load_meta
+    // Q rows of the group, issued first so they overlap the record-table
+    // hop: wave 0 loads 16-byte pieces L = lane, lane + 64 (row L / 16, u32
+    // pairs 4 (L % 16) .. + 3); rows >= group are zero.
+    uint4 qv[2];
+    if (w == 0) {
+      // a buffer resource over the group's rows: pieces past them read zero
+      const rsrc_t rq = make_rsrc(p.q + (int64_t)b * p.q_stride + (int64_t)h * p.group * kDim, p.group * kDim * 2);
+      qv[0] = bld16(rq, 16 * lane, 0);
+      qv[1] = bld16(rq, 16 * lane, 1024);
+    }
+    // block ids of the unit's first 64 pages (one per lane), in the same hop
+    // as page 0's record tables, which come straight from the descriptor's
+    // block id
+    const int blk = load_block(bt, 0, npages, lane);
     RecRef kr, vr;
     {
       const int64_t kidx = ((int64_t)blk0 * 2) * p.kvh + h;
-      const int64_t ka = uniform64(p.rec_addr[kidx]), va = uniform64(p.rec_addr[kidx + p.kvh]);
-      kr = make_ref((uint32_t)ka, (uint32_t)((uint64_t)ka >> 32), uniform(p.rec_len[kidx]));
-      vr = make_ref((uint32_t)va, (uint32_t)((uint64_t)va >> 32), uniform(p.rec_len[kidx + p.kvh]));
+      const int64_t ka = p.rec_addr[kidx], va = p.rec_addr[kidx + p.kvh];
+      const int kl = p.rec_len[kidx], vl = p.rec_len[kidx + p.kvh];
+      asm volatile("" ::"v"(ka), "v"(va), "v"(kl), "v"(vl));  // all four in one hop
+      kr = make_ref((uint32_t)uniform64(ka), (uint32_t)((uint64_t)uniform64(ka) >> 32), uniform(kl));
+      vr = make_ref((uint32_t)uniform64(va), (uint32_t)((uint64_t)uniform64(va) >> 32), uniform(vl));
     }
-    PageMeta meta = load_meta(p, bt, 0, npages, h, lane);
+    // page 0: dense K slab and both variable regions, in flight before the
+    // workgroup synchronises; then the metadata of the unit's other pages
+    SlabBuf fk, fv;
+    prefetch_dense(kr, w, nt, fk);
+    uint2 vk = prefetch_var(kr, w, lane), vv = prefetch_var(vr, w, lane);
+    PageMeta meta = load_meta(p, blk, h);
 
     __syncthreads();  // the previous unit is done with every tile
     FP_STAMP(1);
-    // Q tile: lane (c, n < 8) of wave 0 writes its four 16-byte fragments;
-    // the dims of slot i = 4x + 2f + e of (a, c) are 32a + 16x + 8f + 2c + e.
-    if (w == 0 && hh == 0) {
-      const bool valid = n < p.group;
-      const uint32_t* q = reinterpret_cast<const uint32_t*>(p.q + (int64_t)b * p.q_stride +
-                                                            (int64_t)(h * p.group + (valid ? n : 0)) * kDim);
+    // Q into the fragment tile: u32 pair j of row r goes to fragment
+    // (r, a = j / 16, c = j % 4) at word x = (j % 16) / 4, i.e. the dims of
+    // slot i = 4x + 2f + e of (a, c) are 32a + 16x + 8f + 2c + e.
+    if (w == 0) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d = 16 * a + c;
-        const uint4 v = valid ? make_uint4(q[d], q[d + 4], q[d + 8], q[d + 12]) : make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(sh.qt + ((n * 4 + a) * 4 + c) * 16) = v;
+      for (int k = 0; k < 2; ++k) {
+        const int L = lane + 64 * k, row = L >> 4;
+        const uint32_t v[4] = {qv[k].x, qv[k].y, qv[k].z, qv[k].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int j = 4 * (L & 15) + t;
+          *reinterpret_cast<uint32_t*>(sh.qt + ((row * 4 + (j >> 4)) * 4 + (j & 3)) * 16 + 4 * ((j >> 2) & 3)) = v[t];
+        }
       }
     }
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-
-    // page 0: dense K slab and both variable regions, staged before the loop
     FP_STAMP(2);
-    SlabBuf fk, fv;
-    prefetch_dense(kr, w, nt, fk);
-    uint2 vk = prefetch_var(kr, w, lane), vv = prefetch_var(vr, w, lane);
     expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
     expand_var(vr, vv, w, lane, vlut.s, sh.esc[0][1], sh.hdr[0][1]);
     __syncthreads();
@@ -608,7 +628,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       const int par = i & 1;
       const bool more = i + 1 < npages;
       const int tok0 = (p0 + i) * kTokens;
-      if (more && ((i + 1) & 63) == 0) meta = load_meta(p, bt, i + 1, npages, h, lane);
+      if (more && ((i + 1) & 63) == 0) meta = load_meta(p, load_block(bt, i + 1, npages, lane), h);
       // V slab of this page in flight while K is decoded; the next page's
       // variable regions in flight for the whole page
       prefetch_dense(vr, w, nt, fv);
@@ -624,9 +644,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      decode_slab(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0],
-                  [&](auto a, const uint4& w0, const uint4& w1) {
-                    const uint4 qa = tile_frag(sh.qt, n, a, c);
+      decode_slab(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0], sh.qt, n, c,
+                  [&](auto a, const uint4& w0, const uint4& w1, const uint4& qa) {
                     s0 = mfma(a_frag(w0, w1, 0), qa, s0);
                     s1 = mfma(a_frag(w0, w1, 1), qa, s1);
                   });
@@ -700,9 +719,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       FP_STAMP(6 + 5 * min(i, 4));
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
-      decode_slab(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1],
-                  [&](auto a, const uint4& w0, const uint4& w1) {
-                    const uint4 pa = tile_frag(sh.pt, n, a, c);
+      decode_slab(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
+                  [&](auto a, const uint4& w0, const uint4& w1, const uint4& pa) {
                     o0 = mfma(a_frag(w0, w1, 0), pa, o0);
                     o1 = mfma(a_frag(w0, w1, 1), pa, o1);
                   });
@@ -743,7 +761,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run, l_all);
     }
     FP_STAMP(28);
-    merge_chunks(p, sh, b, h, first, chunks, unit - first);
+    merge_chunks(p, sh, b, h, first, chunks);
     FP_STAMP(29);
   }
   // rows with no context produce zeros (workgroup 0 of each head)
@@ -761,6 +779,20 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
 using namespace fp;
 
+// Workgroups of attn_kernel resident on the current device at once:
+// kAttnPerCu per compute unit (cached per device).
+static int decode_slots() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = kAttnPerCu * cus;
+  }
+  return cache[dev];
+}
+
 #ifdef FP_TRACE
 extern "C" int fp_trace_read(uint64_t* host, int64_t n) {
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(fp_trace_buf), n * sizeof(uint64_t)) == hipSuccess ? 0 : -1;
@@ -777,7 +809,8 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   FP_CHECK(group == 1 || group == 2 || group == 4 || group == 8, "query heads need a group dividing 8");
   if (batch == 0) return 0;
   FP_CHECK(units >= batch, "decode needs at least one unit per sequence");
-  FP_CHECK(q_stride % 2 == 0 && q_stride >= kv_heads * group * kDim, "q must be [B, H, 128] with contiguous heads");
+  FP_CHECK(q_stride % 8 == 0 && q_stride >= kv_heads * group * kDim && reinterpret_cast<uintptr_t>(q) % 16 == 0,
+           "q must be [B, H, 128] with contiguous heads, 16-byte aligned rows");
   FP_CHECK(out_stride % 2 == 0 && out_stride >= kv_heads * group * kDim && reinterpret_cast<uintptr_t>(out) % 4 == 0,
            "out must be [B, H, 128] with contiguous heads");
   FP_CHECK(opart_elems >= kv_heads * units * 8 * kDim && ml_elems >= kv_heads * units * 16,
@@ -809,12 +842,21 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.ud_off = ud_offset((int)units);
   p.done = plan + p.ud_off + 8 * units;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
+  const int slots = decode_slots();
+  FP_CHECK(slots > 0, "cannot query the device's compute-unit count");
   if (replan) {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan, (int)batch,
-                       (int)units, (int)kv_heads);
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
+                       (int)batch, (int)units, (int)kv_heads, slots);
     FP_LAUNCH_CHECK();
   }
-  hipLaunchKernelGGL(attn_kernel, dim3((unsigned)units, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);
+  // persistent grid: one resident wave of workgroups (slots over all KV
+  // heads) walks the units in use
+#if FP_PERSIST
+  const int64_t per_head = std::min<int64_t>(units, (slots + kv_heads - 1) / kv_heads);
+#else
+  const int64_t per_head = units;
+#endif
+  hipLaunchKernelGGL(attn_kernel, dim3((unsigned)per_head, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);
   FP_LAUNCH_CHECK();
   return 0;
 }

@@ -35,6 +35,9 @@ GQA = 8
 # Split capacity per compute unit: a unit is one 256-thread workgroup and
 # the decode kernel keeps 3 of them resident per CU (3 waves per SIMD).
 UNITS_PER_CU = 3
+# Waves of split capacity in decode_units: the planner may spread a step over
+# up to this many rounds of resident workgroups.
+SPLIT_WAVES = 4
 
 
 @dataclass(frozen=True)
@@ -57,11 +60,12 @@ class RecordTables:
 def decode_units(batch: int, kv_heads: int, num_sms: int) -> int:
     """Work-unit capacity per KV head of a decode launch.
 
-    One unit per sequence plus one wave of split capacity minus one, as in
-    the reference (fused_attn_decode.py:58-85); a "wave" here is the
-    workgroups the device runs at once per KV head: ``UNITS_PER_CU`` per
-    compute unit.  Depends only on the (padded) batch size, so the launch
-    shape is fixed under graph capture.
+    One unit per sequence plus ``SPLIT_WAVES`` waves of split capacity minus
+    one (the reference has one wave, fused_attn_decode.py:58-85); a "wave"
+    is the workgroups the device runs at once per KV head, ``UNITS_PER_CU``
+    per compute unit.  The planner picks how many of them to use.  Depends
+    only on the (padded) batch size, so the launch shape is fixed under graph
+    capture.
 
     Args:
         batch: Number of sequences (padded batch size under graphs).
@@ -72,7 +76,7 @@ def decode_units(batch: int, kv_heads: int, num_sms: int) -> int:
         Unit count, at least ``batch``.
     """
     wave = max(1, (UNITS_PER_CU * num_sms) // max(1, kv_heads))
-    return batch + wave - 1
+    return batch + SPLIT_WAVES * wave - 1
 
 
 def workspace_elems(kv_heads: int, units: int) -> tuple[int, int, int]:

@@ -175,37 +175,40 @@ def paged_attention(q_bits: np.ndarray, heads: int, rec: np.ndarray, rec_off: np
     return out
 
 
-def decode_plan(seq_lens: np.ndarray, units: int) -> tuple[int, int, np.ndarray, np.ndarray]:
-    """Split-KV work plan of the reference planner (fused_attn_decode.cu:95-163).
+def decode_plan(seq_lens: np.ndarray, units: int, kv_heads: int = 1,
+                slots: int = 768) -> tuple[int, int, np.ndarray, np.ndarray]:
+    """Split-KV work plan: the reference planner's layout
+    (fused_attn_decode.cu:95-163) with this build's chunk-size policy.
 
-    Returns ``(ppc, budget, unit_map [units, 2], seq_map [B, 2])``: unit u
+    Every sequence is cut into chunks of ``ppc`` pages.  ``ppc`` minimises
+    ``ceil(chunks * kv_heads / slots) * (ppc + 1)`` over the candidates
+    ``ceil(longest / c)`` for c = 1..64 whose chunk count fits ``units``,
+    ties going to the larger ``ppc`` (``slots``: workgroups the device runs
+    at once over all heads).
+
+    Returns ``(ppc, used, unit_map [units, 2], seq_map [B, 2])``: unit u
     covers pages from ``unit_map[u, 1]`` of sequence ``unit_map[u, 0]`` (-1
     when idle; an idle unit's page entry is left 0 here), sequence b owns
-    ``seq_map[b, 1]`` units from ``seq_map[b, 0]``.
+    ``seq_map[b, 1]`` units from ``seq_map[b, 0]``, ``used`` units in all.
     """
     lens = np.asarray(seq_lens, np.int64)
     batch = lens.size
     pages = (lens + 127) >> 7
-    total, longest, active = int(pages.sum()), int(pages.max(initial=0)), int((pages > 0).sum())
+    longest = int(pages.max(initial=0))
 
     def chunks(ppc: int) -> np.ndarray:
         return (pages + ppc - 1) // ppc
 
-    capacity = max(1, units - batch + active)
-    wave = units - batch + 1
-    budget = min(capacity, max(active, wave))
-    if capacity > budget:
-        tail_bound = 2 * max(1, -(-total // budget))
-        if int(chunks(tail_bound).sum()) > budget:
-            budget = capacity
-    lo, hi = max(1, -(-total // budget)), max(1, longest)
-    while lo < hi:
-        mid = (lo + hi) // 2
-        if int(chunks(mid).sum()) <= budget:
-            hi = mid
-        else:
-            lo = mid + 1
-    ppc = lo
+    best = None
+    for c in range(1, 65):
+        ppc = max(1, -(-longest // c))
+        n = int(chunks(ppc).sum())
+        if n > units:
+            continue
+        key = (-(-n * kv_heads // slots) * (ppc + 1), -ppc)
+        if best is None or key < best:
+            best = key
+    ppc = -best[1]
     c = chunks(ppc)
     first = np.concatenate([[0], np.cumsum(c)[:-1]]).astype(np.int64) if batch else np.zeros(0, np.int64)
     unit_map = np.zeros((units, 2), np.int32)
@@ -214,7 +217,7 @@ def decode_plan(seq_lens: np.ndarray, units: int) -> tuple[int, int, np.ndarray,
         for s in range(int(c[b])):
             unit_map[first[b] + s] = (b, s * ppc)
     seq_map = np.stack([first, c], axis=1).astype(np.int32) if batch else np.zeros((0, 2), np.int32)
-    return ppc, budget, unit_map, seq_map
+    return ppc, int(c.sum()), unit_map, seq_map
 
 
 def num_threads() -> int:

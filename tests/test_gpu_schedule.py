@@ -123,9 +123,14 @@ def _check_outputs(queries, outputs, source, block_table, lengths):
 
 
 def _check_plan(plan, lengths, units):
-    ppc, budget, unit_map, seq_map = oracle.decode_plan(lengths, units)
+    import torch
+
+    from fragpack_amd.ops.fused_attn_decode import UNITS_PER_CU
+
+    slots = UNITS_PER_CU * torch.cuda.get_device_properties(plan.device).multi_processor_count
+    ppc, used, unit_map, seq_map = oracle.decode_plan(lengths, units, HEADS, slots)
     got = plan.cpu().numpy()
-    assert (int(got[0]), int(got[1])) == (ppc, budget)
+    assert (int(got[0]), int(got[1])) == (ppc, used)
     umap = got[2 : 2 + 2 * units].reshape(units, 2).copy()
     umap[umap[:, 0] < 0, 1] = 0  # an idle unit's page entry is unspecified
     np.testing.assert_array_equal(umap, unit_map)

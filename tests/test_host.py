@@ -67,7 +67,7 @@ def test_tables_npz_round_trip(tmp_path):
 
 def test_decode_units_and_workspace():
     assert fad.decode_units(4, 4, 256) >= 4
-    assert fad.decode_units(269, 4, 256) == 269 + fad.UNITS_PER_CU * 256 // 4 - 1
+    assert fad.decode_units(269, 4, 256) == 269 + fad.SPLIT_WAVES * (fad.UNITS_PER_CU * 256 // 4) - 1
     opart, ml, plan = fad.workspace_elems(4, 100)
     assert opart == 4 * 100 * 8 * 128 and ml == 4 * 100 * 16
     assert plan >= 2 + 4 * 100 + 8 * 100 + 4 * 100

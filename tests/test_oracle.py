@@ -171,25 +171,35 @@ def test_paged_attention_repetition_identity():
     np.testing.assert_allclose(got, want, atol=1e-4, rtol=1e-4)
 
 
-def _brute_min_ppc(pages: np.ndarray, budget: int) -> int:
-    return next(p for p in range(1, int(pages.max(initial=0)) + 2) if ((pages + p - 1) // p).sum() <= budget)
+def _plan_cost(pages: np.ndarray, ppc: int, heads: int, slots: int) -> tuple[int, int]:
+    """Modelled makespan of a chunk size: rounds of resident workgroups
+    times (chunk pages + one page of fixed unit cost), by direct counting."""
+    n = sum(-(-int(x) // ppc) for x in pages)
+    return -(-n * heads // slots) * (ppc + 1), n
 
 
 @pytest.mark.parametrize("seed", range(6))
 def test_decode_plan_invariants(seed):
-    """The planner restatement against brute force: ppc is the smallest chunk
-    size whose chunks fit the budget, the budget lies between the live rows
-    and the capacity, and the unit map tiles every sequence's pages once."""
+    """The planner restatement against brute force over its candidate set:
+    the chosen chunk size fits the unit cap, no candidate has a lower
+    modelled cost (ties: no larger chunk with the same cost), and the unit
+    map tiles every sequence's pages exactly once."""
     rng = np.random.default_rng(seed)
     batch = int(rng.integers(1, 300))
     lens = rng.integers(0, 40000, batch).astype(np.int32)
     lens[rng.random(batch) < 0.2] = 0
     units = batch + int(rng.integers(0, 600))
-    ppc, budget, unit_map, seq_map = oracle.decode_plan(lens, units)
+    heads, slots = int(rng.choice([1, 4, 8, 32])), 768
+    ppc, used, unit_map, seq_map = oracle.decode_plan(lens, units, heads, slots)
     pages = (lens.astype(np.int64) + 127) // 128
-    active = int((pages > 0).sum())
-    assert max(1, min(active, units - batch + 1)) <= budget <= max(1, units - batch + active)
-    assert ppc == _brute_min_ppc(pages, budget)
+    longest = int(pages.max(initial=0))
+    cost, n = _plan_cost(pages, ppc, heads, slots)
+    assert n == used <= units
+    for c in range(1, 65):
+        cand = max(1, -(-longest // c))
+        cc, cn = _plan_cost(pages, cand, heads, slots)
+        if cn <= units:
+            assert cc > cost or (cc == cost and cand <= ppc)
     covered = np.zeros(int(pages.sum()), np.int64)
     offs = np.concatenate([[0], np.cumsum(pages)])
     for u, (b, p0) in enumerate(unit_map):
@@ -204,16 +214,22 @@ def test_decode_plan_invariants(seed):
 
 
 def test_decode_plan_known_answers():
-    """Hand-computed plans.  4 x 64 pages with 195 units: budget 192 (one wave
-    of splits), tail bound 4 keeps it, smallest ppc with 4*ceil(64/ppc) <= 192
-    is 2.  Minimum units (one per row) give one chunk per live row.  An all-empty
-    batch of 5 rows with 7 units: capacity max(1, 7-5+0) = 2, no chunks."""
-    ppc, budget, unit_map, seq_map = oracle.decode_plan(np.full(4, 8192, np.int32), 195)
-    assert (ppc, budget) == (2, 192)
+    """Hand-computed plans on a 768-slot device.  Config 1 (4 x 64 pages, 4
+    heads): ppc 2 gives 128 units per head = 512 workgroups, one round, cost
+    3; ppc 1 needs two rounds (cost 4).  Config 4's decode (64 x 256 pages, 8
+    heads): ppc 86 gives 3 chunks per row, 1536 workgroups in two rounds,
+    cost 174, against 257 for one chunk per row.  Units equal to the batch
+    cap the chunks: pages [3, 0, 71, 1] with 4 units take ppc 36 (4 chunks,
+    cost 37; ppc 24 would need 5).  An all-empty batch plans nothing."""
+    ppc, used, unit_map, seq_map = oracle.decode_plan(np.full(4, 8192, np.int32), 4 + 4 * 192 - 1, 4, 768)
+    assert (ppc, used) == (2, 128)
     assert seq_map.tolist() == [[0, 32], [32, 32], [64, 32], [96, 32]]
     assert unit_map[33].tolist() == [1, 2] and unit_map[128, 0] == -1
+    ppc, used, _, seq_map = oracle.decode_plan(np.full(64, 32768, np.int32), 64 + 4 * 96 - 1, 8, 768)
+    assert (ppc, used) == (86, 192) and np.all(seq_map[:, 1] == 3)
     lens = np.array([300, 0, 9000, 1], np.int32)
-    ppc, budget, _, seq_map = oracle.decode_plan(lens, 4)
-    assert budget == 3 and ppc == 71 and seq_map[:, 1].tolist() == [1, 0, 1, 1]
-    ppc, budget, unit_map, seq_map = oracle.decode_plan(np.zeros(5, np.int32), 7)
-    assert budget == 2 and ppc == 1 and np.all(unit_map[:, 0] == -1) and not seq_map[:, 1].any()
+    ppc, used, _, seq_map = oracle.decode_plan(lens, 4, 4, 768)
+    assert used == 4 and ppc == 36 and seq_map[:, 1].tolist() == [1, 0, 2, 1]
+    ppc, used, unit_map, seq_map = oracle.decode_plan(np.zeros(5, np.int32), 7, 4, 768)
+    assert used == 0 and ppc == 1 and np.all(unit_map[:, 0] == -1) and not seq_map[:, 1].any()
+
