@@ -66,7 +66,7 @@ struct AttnParams {
   const uint8_t* slut;
   const int32_t* block_table;
   const int32_t* seq_lens;
-  const int32_t* plan;
+  int32_t* plan;
   float* opart;
   float* ml;
   uint16_t* out;
@@ -76,6 +76,8 @@ struct AttnParams {
   int64_t bt_stride;  // entries between block-table rows
   int kvh, group, units, batch;
   int ud_off;  // int32 offset of the unit descriptors in plan
+  int slots;   // resident workgroups of this kernel on the device
+  int inline_plan;  // 1: every workgroup plans for itself (batch <= 64)
   float scale_log2;
 };
 
@@ -472,6 +474,49 @@ struct AttnShared {
   int last;
 };
 
+// The planner of plan_kernel, run by a single wavefront for batch <= 64
+// (sequence b in lane b): lane c scores candidate ppc = ceil(longest / (c+1))
+// with the same cost and tie rule, then every lane holds its sequence's page
+// count, first unit and chunk count.  Used when the attention kernel plans
+// for itself (no separate plan launch).
+struct InlinePlan {
+  int len, n, first, cnt;  // per lane (sequence = lane)
+  int ppc, used;           // uniform
+};
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)x, o, 64), hi = __shfl_xor((uint32_t)(x >> 32), o, 64);
+    const uint64_t y = ((uint64_t)hi << 32) | lo;
+    x = y < x ? y : x;
+  }
+  return x;
+}
+
+__device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane) {
+  InlinePlan r;
+  r.len = lane < p.batch ? p.seq_lens[lane] : 0;
+  r.n = (r.len + 127) >> 7;
+  const int longest = wave_total<true>(r.n);
+  const int cand = max(1, (longest + lane) / (lane + 1));
+  const Divider dv(cand);
+  int chunks = 0;
+  for (int b = 0; b < p.batch; ++b) chunks += dv.chunks(__builtin_amdgcn_readlane(r.n, b));
+  uint64_t key = ~0ull;
+  if (chunks <= p.units) {
+    const int64_t rounds = ((int64_t)chunks * p.kvh + p.slots - 1) / p.slots;
+    key = ((uint64_t)(rounds * (cand + kUnitCost)) << 24) | (uint64_t)(0xFFFFFF - cand);
+  }
+  key = wave_min_u64(key);
+  r.ppc = uniform(0xFFFFFF - (int)(key & 0xFFFFFFu));
+  r.cnt = Divider(r.ppc).chunks(r.n);
+  const int incl = wave_scan_dpp<false>(r.cnt);
+  r.first = incl - r.cnt;
+  r.used = __builtin_amdgcn_readlane(incl, 63);
+  return r;
+}
+
 // Split-KV merge of (b, h) after this workgroup wrote the partial of one of
 // its ``chunks`` units (``first`` .. ``first + chunks - 1``): the last
 // workgroup to arrive merges all of them with the online-softmax merge in the
@@ -543,6 +588,7 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
       make_uint2(lo, hi);
 }
 
+template <bool kInlinePlan>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FP_ATTN_WAVES_PER_EU))) attn_kernel(AttnParams p) {
   __shared__ AttnShared sh;
   const int lane = wave_lane();
@@ -552,21 +598,71 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const int nt = 32 * hh + 4 * g + c;
   const NatPerm np{4 * lane_of_natural(lane), 4 * nt};
   const int n = lane & 15;  // MFMA column = query head within the group
-  const int used = uniform(p.plan[1]);  // units in use
   const HeadLut klut = load_lut(p.plut, p.slut, h);
   const HeadLut vlut = load_lut(p.plut, p.slut, p.kvh + h);
 
   FP_STAMP(0);
+  // the work plan: planned here (inline) or read from the plan workspace
+  InlinePlan ip{0, 0, 0, 0, 1, 0};
+  if constexpr (kInlinePlan) ip = inline_plan(p, lane);
+  const int used = kInlinePlan ? ip.used : uniform(p.plan[1]);  // units in use
+  if (kInlinePlan && blockIdx.x == 0 && h == 0 && w == 0) {
+    // the plan words for later calls that reuse this plan
+    int32_t* plan = p.plan;
+    if (lane < p.batch) {
+      plan[2 + 2 * p.units + 2 * lane] = ip.first;
+      plan[3 + 2 * p.units + 2 * lane] = ip.cnt;
+    }
+    if (lane == 0) {
+      plan[0] = ip.ppc;
+      plan[1] = ip.used;
+    }
+  }
+  if (kInlinePlan && h == 0) {
+    // idle units of this workgroup's stride
+    int32_t* plan = p.plan;
+    for (int u = blockIdx.x + gridDim.x * (int)threadIdx.x; u < p.units; u += gridDim.x * 64 * kWaves)
+      if (u >= used) {
+        plan[2 + 2 * u] = -1;
+        plan[p.ud_off + 8 * u] = -1;
+      }
+  }
   for (int unit = blockIdx.x; unit < used; unit += gridDim.x) {
-    // unit descriptor: b, first page, pages, context, first unit of b,
-    // chunks of b, block of page 0 (both halves loaded together)
-    const int4* udp = reinterpret_cast<const int4*>(p.plan + p.ud_off + 8 * unit);
-    const int4 u0 = udp[0], u1 = udp[1];
-    asm volatile("" ::"v"(u0.x), "v"(u0.y), "v"(u0.z), "v"(u0.w), "v"(u1.x), "v"(u1.y), "v"(u1.z));  // one hop
-    const int b = uniform(u0.x);
-    if (b < 0) continue;
-    const int p0 = uniform(u0.y), npages = uniform(u0.z), seq = uniform(u0.w);
-    const int first = uniform(u1.x), chunks = uniform(u1.y), blk0 = uniform(u1.z);
+    int b, p0, npages, seq, first, chunks, blk0;
+    if constexpr (kInlinePlan) {
+      // the last live sequence whose first unit is <= unit owns it
+      const uint64_t own = __ballot(lane < p.batch && ip.cnt > 0 && ip.first <= unit);
+      b = 63 - __builtin_clzll(own);
+      first = __builtin_amdgcn_readlane(ip.first, b);
+      chunks = __builtin_amdgcn_readlane(ip.cnt, b);
+      seq = __builtin_amdgcn_readlane(ip.len, b);
+      p0 = (unit - first) * ip.ppc;
+      npages = min(__builtin_amdgcn_readlane(ip.n, b), p0 + ip.ppc) - p0;
+      blk0 = uniform(p.block_table[(int64_t)b * p.bt_stride + p0]);
+      if (h == 0 && threadIdx.x == 0) {
+        // this unit's plan entries for later calls
+        int32_t* plan = p.plan;
+        plan[2 + 2 * unit] = b;
+        plan[3 + 2 * unit] = p0;
+        int4* ud = reinterpret_cast<int4*>(plan + p.ud_off + 8 * unit);
+        ud[0] = make_int4(b, p0, npages, seq);
+        ud[1] = make_int4(first, chunks, blk0, npages > 1 ? p.block_table[(int64_t)b * p.bt_stride + p0 + 1] : 0);
+      }
+    } else {
+      // unit descriptor: b, first page, pages, context, first unit of b,
+      // chunks of b, block of page 0 (both halves loaded together)
+      const int4* udp = reinterpret_cast<const int4*>(p.plan + p.ud_off + 8 * unit);
+      const int4 u0 = udp[0], u1 = udp[1];
+      asm volatile("" ::"v"(u0.x), "v"(u0.y), "v"(u0.z), "v"(u0.w), "v"(u1.x), "v"(u1.y), "v"(u1.z));  // one hop
+      b = uniform(u0.x);
+      if (b < 0) continue;
+      p0 = uniform(u0.y);
+      npages = uniform(u0.z);
+      seq = uniform(u0.w);
+      first = uniform(u1.x);
+      chunks = uniform(u1.y);
+      blk0 = uniform(u1.z);
+    }
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
     // Q rows of the group, issued first so they overlap the record-table
     // hop: wave 0 loads 16-byte pieces L = lane, lane + 64 (row L / 16, u32
@@ -767,7 +863,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
     for (int b = w; b < p.batch; b += kWaves) {
-      if (p.plan[3 + 2 * p.units + 2 * b] != 0) continue;
+      const int cnt = kInlinePlan ? __builtin_amdgcn_readlane(ip.cnt, b) : p.plan[3 + 2 * p.units + 2 * b];
+      if (cnt != 0) continue;
       uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)h * p.group * kDim);
       for (int x = lane; x < p.group * kDim / 2; x += 64) orow[x] = 0u;
     }
@@ -844,7 +941,11 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   const int slots = decode_slots();
   FP_CHECK(slots > 0, "cannot query the device's compute-unit count");
-  if (replan) {
+  p.slots = slots;
+  // replan 2: plan inside the attention kernel (batch <= 64; the merge
+  // counters must be as a previous completed call left them, i.e. zero)
+  p.inline_plan = replan == 2 && batch <= 64;
+  if (replan && !p.inline_plan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
                        (int)batch, (int)units, (int)kv_heads, slots);
     FP_LAUNCH_CHECK();
@@ -856,7 +957,10 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
 #else
   const int64_t per_head = units;
 #endif
-  hipLaunchKernelGGL(attn_kernel, dim3((unsigned)per_head, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);
+  if (p.inline_plan)
+    hipLaunchKernelGGL(attn_kernel<true>, dim3((unsigned)per_head, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);
+  else
+    hipLaunchKernelGGL(attn_kernel<false>, dim3((unsigned)per_head, (unsigned)kv_heads), dim3(64 * kWaves), 0, stream, p);
   FP_LAUNCH_CHECK();
   return 0;
 }

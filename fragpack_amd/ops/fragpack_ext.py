@@ -137,7 +137,7 @@ class Extension:
         # one tuple read per tensor property: this runs once per decode layer
         qsh, qst, ost, bst = q.shape, q.stride(), out.stride(), block_table.stride()
         bf16, i32 = torch.bfloat16, torch.int32
-        _check(len(qsh) == 3 and qsh[2] == 128 and qst[2] == 1 and qst[1] == 128 and qst[0] % 2 == 0
+        _check(len(qsh) == 3 and qsh[2] == 128 and qst[2] == 1 and qst[1] == 128 and qst[0] % 8 == 0
                and q.dtype == bf16, "q must be [B, H, 128] with contiguous heads")
         _check(len(ost) == 3 and ost[2] == 1 and ost[1] == 128 and out.dtype == bf16 and out.shape[1] == qsh[1],
                "out must be [B, H, 128] with contiguous heads")
@@ -151,14 +151,22 @@ class Extension:
         _check(kvh * group == qsh[1], "query heads must be a multiple of the group")
         if B == 0:
             return
+        # Replanning runs inside the attention kernel (no plan launch) once a
+        # call has left this workspace's merge counters at zero; the first
+        # call on a workspace launches the planner, which zeroes them.
+        mode = 0
+        if replan:
+            mode = 2 if getattr(plan, "_fp_counters_zeroed", False) else 1
         if self._fused(
             _dev(q, "q"), qst[0], B, kvh, group, _dev(rec_addr, "rec_addr"), _dev(rec_len, "rec_len"),
             _dev(plut, "plut"), _dev(slut, "slut"), _dev(block_table, "block_table"), bst[0],
             _dev(seq_lens, "seq_lens"), _dev(opart, "opart"), opart.numel(), _dev(ml, "ml"), ml.numel(),
-            _dev(plan, "plan"), plan.numel(), _dev(out, "out"), ost[0], units, replan, scale,
+            _dev(plan, "plan"), plan.numel(), _dev(out, "out"), ost[0], units, mode, scale,
             torch.cuda.current_stream().cuda_stream,
         ):
             raise RuntimeError(f"fp_fused_decode: {self._lib.fp_last_error().decode()}")
+        if mode:
+            plan._fp_counters_zeroed = True
 
     # -- store (fragpack_ext.cpp:11-39, hbm_kv.cu:669-734) --
     def hbm_prepare(self, *args) -> None:

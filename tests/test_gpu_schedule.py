@@ -236,3 +236,55 @@ def test_plan_beyond_lds_table(encoded_store):
     torch.cuda.synchronize()
     _check_plan(ws[2], lengths, units)
     _check_outputs(queries, outputs, source, table, lengths)
+
+
+@pytest.mark.parametrize("group", [1, GQA])
+def test_small_batch_plans_inside_the_attention_kernel(encoded_store, group):
+    """Batches of at most 64 rows replan inside the attention kernel once the
+    workspace's merge counters are known to be zero (after its first call).
+    Successive calls with changed lengths, then a captured graph replayed
+    over new lengths: outputs match fp32 attention and the plan words match
+    the planner restatement every time."""
+    import torch
+
+    from fragpack_amd.ops.fused_attn_decode import decode_units
+
+    store, _arenas, source = encoded_store
+    batch = 40
+    print("schedule inline plan", batch, group, flush=True)
+    table = _block_table(batch)
+    rng = np.random.default_rng(40 + group)
+    sms = torch.cuda.get_device_properties(source.device).multi_processor_count
+    units = decode_units(batch, HEADS, sms)
+    ws = _workspace(units, source.device)
+    dev_table = torch.from_numpy(table).to(source.device)
+    gen = torch.Generator(device=source.device).manual_seed(4040 + group)
+    queries = [torch.randn(batch, HEADS * group, DIM, dtype=torch.bfloat16, device=source.device, generator=gen)
+               for _ in range(LAYERS)]
+    outputs = [torch.full_like(q, float("nan")) for q in queries]
+    cases = [_ragged_lengths(batch), rng.integers(0, 200 * TOKENS, batch).astype(np.int32),
+             np.zeros(batch, np.int32), np.full(batch, 9 * TOKENS + 5, np.int32)]
+    cases[1][::3] = 0
+    dev_lengths = torch.from_numpy(cases[0]).to(source.device)
+    for lengths in cases:
+        dev_lengths.copy_(torch.from_numpy(lengths))
+        for out in outputs:
+            out.fill_(float("nan"))
+        _decode_layers(store, queries, outputs, dev_table, dev_lengths, units, ws)
+        torch.cuda.synchronize()
+        _check_outputs(queries, outputs, source, table, lengths)
+        _check_plan(ws[2], lengths, units)
+    assert getattr(ws[2], "_fp_counters_zeroed", False)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        _decode_layers(store, queries, outputs, dev_table, dev_lengths, units, ws)
+    for lengths in reversed(cases):
+        dev_lengths.copy_(torch.from_numpy(lengths))
+        for out in outputs:
+            out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        _check_outputs(queries, outputs, source, table, lengths)
+        _check_plan(ws[2], lengths, units)
