@@ -406,6 +406,8 @@ def main() -> None:
     ap.add_argument("--prefill-seqs", type=int, default=4)
     ap.add_argument("--prefill-len", type=int, default=8192)
     ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--no-large", action="store_true", help="skip the config-4 decode shape leg")
+    ap.add_argument("--large-steps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3x (scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -437,6 +439,23 @@ def main() -> None:
             res.pop(k)
         torch.cuda.empty_cache()
         raw = decode_bench(torch, args, raw=True)
+    large = large_raw = None
+    if not args.no_large:
+        # config 4's decode sweep shape: B64 x H8 x G4 x 32768 context
+        largs = argparse.Namespace(**vars(args))
+        largs.batch, largs.heads, largs.group, largs.context = 64, 8, 4, 32768
+        largs.steps, largs.warmup, largs.units = args.large_steps, 3, 0
+        for r in (res, raw):
+            if r is not None:
+                for k in ("store", "arena"):
+                    r.pop(k, None)
+        torch.cuda.empty_cache()
+        large = decode_bench(torch, largs)
+        for k in ("store", "arena"):
+            large.pop(k)
+        torch.cuda.empty_cache()
+        if not args.no_raw_arm:
+            large_raw = decode_bench(torch, largs, raw=True)
     step_s = res["step_ms"] / 1e3
     kern_s = res["kern_ms"] / 1e3
     achieved = res["algo_bytes"] / kern_s / 1e9
@@ -484,6 +503,23 @@ def main() -> None:
             "us_per_step": round(raw["step_ms"] * 1e3, 2), "kernel_us": round(raw["kern_ms"] * 1e3, 2),
             "validated": raw["valid"], "compressed_step_speedup": round(raw["step_ms"] / res["step_ms"], 3),
             "hbm_GBps": round(raw["algo_bytes"] / (raw["kern_ms"] / 1e3) / 1e9, 1)}
+    if large is not None:
+        lk = large["kern_ms"] / 1e3
+        la = large["algo_bytes"] / lk / 1e9
+        line["decode_large"] = {
+            "workload": "config 4 decode sweep: B64 x H8 x G4 x 32768 ctx, head_dim 128, one layer",
+            "us_per_step": round(large["step_ms"] * 1e3, 1), "kernel_us": round(large["kern_ms"] * 1e3, 1),
+            "units": large["units"], "validated": large["valid"], "max_abs_err": large["max_err"],
+            "effective_GBps": round(large["eff_bytes"] / lk / 1e9, 1), "compression": round(large["comp_ratio"], 4),
+            "roofline": {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(la, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(la / HBM_PEAK_GBS, 4),
+                         "algo_bytes_per_launch": large["algo_bytes"]}}
+        if large_raw is not None:
+            line["decode_large"]["bf16_paged_arm"] = {
+                "us_per_step": round(large_raw["step_ms"] * 1e3, 1),
+                "kernel_us": round(large_raw["kern_ms"] * 1e3, 1), "validated": large_raw["valid"],
+                "compressed_step_speedup": round(large_raw["step_ms"] / large["step_ms"], 3),
+                "hbm_GBps": round(large_raw["algo_bytes"] / (large_raw["kern_ms"] / 1e3) / 1e9, 1)}
     if enc is not None:
         line["encode"] = {"workload": f"config 3 shape: {args.encode_blocks} blocks x 8 KV heads x K/V, 10% "
                                       "Student-t(2)x16, overflow 8192",
