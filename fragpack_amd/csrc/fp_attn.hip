@@ -93,28 +93,6 @@ __device__ __forceinline__ int pages_of(const int32_t* seq_lens, int b) { return
 
 __device__ __forceinline__ int chunks_of(int pages, int ppc) { return (pages + ppc - 1) / ppc; }
 
-// Wavefront-wide inclusive scan with DPP (row shifts within 16-lane rows,
-// then row broadcasts), no LDS round trips.  ``Op`` is + or max over values
-// whose identity is 0.
-template <bool kMax>
-__device__ __forceinline__ int dpp_op(int a, int b) {
-  return kMax ? max(a, b) : a + b;
-}
-template <bool kMax>
-__device__ __forceinline__ int wave_scan_dpp(int x) {
-  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true));  // row_shr:1
-  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true));  // row_shr:2
-  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true));  // row_shr:4
-  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true));  // row_shr:8
-  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
-  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
-  return x;
-}
-template <bool kMax>
-__device__ __forceinline__ int wave_total(int x) {
-  return __builtin_amdgcn_readlane(wave_scan_dpp<kMax>(x), 63);
-}
-
 // Work plan (layout of the reference planner, fused_attn_decode.cu:48-163;
 // policy of this build).  Every sequence is cut into chunks of ``ppc``
 // pages.  The reference takes the smallest ``ppc`` whose chunks fit one wave

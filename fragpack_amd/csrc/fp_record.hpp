@@ -83,16 +83,30 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront.
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = wave_lane();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int n = __shfl_up(v, o, 64);
-    if (lane >= o) v += n;
-  }
-  return v;
+// Wavefront-wide inclusive scan with DPP (row shifts within 16-lane rows,
+// then row broadcasts), no LDS round trips.  ``Op`` is + or max over values
+// whose identity is 0.
+template <bool kMax>
+__device__ __forceinline__ int dpp_op(int a, int b) {
+  return kMax ? max(a, b) : a + b;
 }
+template <bool kMax>
+__device__ __forceinline__ int wave_scan_dpp(int x) {
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true));  // row_shr:1
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true));  // row_shr:2
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true));  // row_shr:4
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true));  // row_shr:8
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  x = dpp_op<kMax>(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return x;
+}
+template <bool kMax>
+__device__ __forceinline__ int wave_total(int x) {
+  return __builtin_amdgcn_readlane(wave_scan_dpp<kMax>(x), 63);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ int wave_incl_scan(int v) { return wave_scan_dpp<false>(v); }
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll

@@ -38,7 +38,7 @@ enum : int { kTagLive = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
 
 constexpr int kPrepThreads = 1024;
 constexpr int kThreads = 256;
-constexpr int kEncodeWgPerCu = 3;  // resident encode workgroups per CU (VGPR-bound; LDS stage 32 KB each)
+constexpr int kEncodeWgPerCu = 4;  // resident encode workgroups per CU (LDS: 32 KB stage + 6 KB each)
 
 struct Store {
   int32_t* counters;
@@ -289,13 +289,27 @@ __global__ void __launch_bounds__(kThreads) write_kernel(Store s, const uint16_t
 // Record encoder core: one 256-thread workgroup, thread t holding the 8
 // kernel-order words of thread t.  Computes codes, counts, the variable
 // region (in LDS) and whether the record codes.
+//
+// The per-(kv, head) lookup table in LDS maps a high byte to
+// code | nib << 4: code = min(rank, 7) (7 = escape), nib = the escape nibble
+// (extended-table index rank - 7, or 15 for a raw scalar; 0 for a primary).
+// A word's eight table bytes are read two per VGPR (16-bit halves) and
+// rearranged with two v_perm into code and nibble words whose nibble j
+// belongs to scalar j, so the rest of the analysis runs 8 scalars per op.
 
 struct EncShared {
-  uint8_t rank[256];
+  uint8_t tb[256];                 // high byte -> code | nib << 4
+  uint8_t esc[kMaxEscapes + 16];   // escape nibbles as bytes, by ordinal
   uint32_t var32[kVarCap / 4];
   int wsum[2][8];  // per 32-thread slab: escapes, raws
   int s_off, s_ovf;
 };
+
+// LDS table entry of rank r (the store's rank_of byte: 0..21, 255 absent).
+__device__ __forceinline__ uint8_t table_byte(uint32_t r) {
+  return r < (uint32_t)kPrimaryDirect ? (uint8_t)r
+                                      : (uint8_t)(kPrimaryDirect | (min(r - kPrimaryDirect, (uint32_t)kRawNibble) << 4));
+}
 
 struct EncResult {
   bool codes;
@@ -304,41 +318,54 @@ struct EncResult {
   int etot, rtot;
 };
 
-// Per-thread symbol words, escape / raw masks; then totals across the
-// workgroup.  Leaves the escape/raw exclusive prefixes of this thread in
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+
+// Code and escape-nibble words of word ``st`` (nibble j = scalar j).
+__device__ __forceinline__ void enc_word(const uint4& w, const uint8_t* tb, uint32_t& code, uint32_t& nib) {
+  // scalar e is the half e & 1 of dword e >> 1; high byte = bits 8..15 / 24..31
+  u16x2_t x0, x1, x2, x3;  // [t0, t2], [t4, t6], [t1, t3], [t5, t7]
+  x0.x = tb[(w.x >> 8) & 0xFF];
+  x0.y = tb[(w.y >> 8) & 0xFF];
+  x1.x = tb[(w.z >> 8) & 0xFF];
+  x1.y = tb[(w.w >> 8) & 0xFF];
+  x2.x = tb[w.x >> 24];
+  x2.y = tb[w.y >> 24];
+  x3.x = tb[w.z >> 24];
+  x3.y = tb[w.w >> 24];
+  const uint32_t g = perm(__builtin_bit_cast(uint32_t, x1), __builtin_bit_cast(uint32_t, x0), 0x06040200u);
+  const uint32_t h = perm(__builtin_bit_cast(uint32_t, x3), __builtin_bit_cast(uint32_t, x2), 0x06040200u);
+  // g = [t0, t2, t4, t6], h = [t1, t3, t5, t7]
+  code = (g & 0x0F0F0F0Fu) | ((h << 4) & 0xF0F0F0F0u);
+  nib = ((g >> 4) & 0x0F0F0F0Fu) | (h & 0xF0F0F0F0u);
+}
+
+// Escape bits (bit 4j set iff scalar j escapes) of a code word.
+__device__ __forceinline__ uint32_t esc_nibbles(uint32_t code) { return ((code + 0x11111111u) >> 3) & 0x11111111u; }
+// Raw bits (bit 4j set iff scalar j's escape nibble is 15) of a nibble word.
+__device__ __forceinline__ uint32_t raw_nibbles(uint32_t nib) {
+  const uint32_t t = nib & (nib >> 2);
+  return t & (t >> 1) & 0x11111111u;
+}
+
+// Per-thread code / nibble words and symbol words; totals across the
+// workgroup.  Leaves the escape / raw exclusive prefixes of this thread in
 // eo / ro.
 __device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared& sh, uint32_t (&sym)[6],
-                                                 uint32_t (&en)[8], uint64_t& emask, uint64_t& rmask, int& eo,
-                                                 int& ro) {
+                                                 uint32_t (&code)[8], uint32_t (&nib)[8], int& eo, int& ro) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-  for (int i = 0; i < 6; ++i) sym[i] = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) en[i] = 0;
-  emask = 0;
-  rmask = 0;
+  int ne = 0, nr = 0;
 #pragma unroll
   for (int st = 0; st < 8; ++st) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sc = 8 * st + e, gi = sc >> 5, sg = sc & 31;
-      const uint32_t val = (u4(wd[st], e >> 1) >> (16 * (e & 1))) & 0xffffu;
-      const int r = sh.rank[val >> 8];
-      const uint32_t code = r < kPrimaryDirect ? (uint32_t)r : (uint32_t)kPrimaryDirect;
-      if (sg < 24) {
-        sym[3 * gi + (sg >> 3)] |= code << (4 * (sg & 7));
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < 3; ++kk) sym[3 * gi + kk] |= ((code >> kk) & 1u) << (4 * (sg - 24) + 3);
-      }
-      if (r >= kPrimaryDirect) emask |= 1ull << sc;
-      if (r >= kTableEntries) rmask |= 1ull << sc;
-      // escape nibble: extended-table index, or 15 for a raw scalar
-      const uint32_t nib = r < kPrimaryDirect ? 0u : r < kTableEntries ? (uint32_t)(r - kPrimaryDirect) : (uint32_t)kRawNibble;
-      en[st] |= nib << (4 * e);
-    }
+    enc_word(wd[st], sh.tb, code[st], nib[st]);
+    ne += __builtin_popcount(esc_nibbles(code[st]));
+    nr += __builtin_popcount(raw_nibbles(nib[st]));
   }
-  const int ne = __popcll(emask), nr = __popcll(rmask);
+  // symbol words of group gi: words 4 gi + k (k < 3), bit 3 of nibble j =
+  // bit k of the code of scalar 24 + j (word 4 gi + 3)
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) sym[3 * gi + k] = code[4 * gi + k] | ((code[4 * gi + 3] << (3 - k)) & 0x88888888u);
   const int ei = wave_incl_scan(ne), ri = wave_incl_scan(nr);
   // per 32-thread slab totals (two per wavefront)
   const int e31 = __shfl(ei, 31, 64), e63 = __shfl(ei, 63, 64);
@@ -373,43 +400,32 @@ __device__ __forceinline__ EncResult enc_analyse(const uint4 (&wd)[8], EncShared
 }
 
 // Builds the variable region in sh.var32 (coded records only).  Caller
-// zeroed sh.var32 before enc_analyse's barrier.
-__device__ __forceinline__ void enc_var(const uint4 (&wd)[8], const uint32_t (&en)[8], EncShared& sh,
-                                        const EncResult& res, uint64_t emask, int eo, int ro) {
-  // Nibbles of this thread's escapes are contiguous in the stream (escape
-  // ordinals eo ..): gather them per 32-bit stream word in a register and
-  // OR each word into LDS once (only words shared with a neighbour thread
-  // need the atomic).  Word st's escapes are visited with static st so the
-  // data words stay in registers; the nibbles come from the analysis.
-  int bitpos = 8 * kHeaderBytes + 4 * eo;
-  int acc_word = bitpos >> 5;
-  uint32_t acc = 0;
-  static_for<0, 8>([&](auto st_c) {
-    constexpr int st = decltype(st_c)::value;
-    uint32_t m = (uint32_t)(emask >> (8 * st)) & 0xFFu;
-    const uint32_t nw = en[st];
+// zeroed sh.var32 before enc_analyse's barrier.  Each thread writes its
+// escape nibbles as bytes at their ordinals (sh.esc) and its raw-list
+// entries; after a barrier the byte stream is packed two nibbles per byte
+// into the region.  Ends with the region complete (barrier).
+__device__ __forceinline__ void enc_var(const uint4 (&wd)[8], const uint32_t (&code)[8], const uint32_t (&nib)[8],
+                                        EncShared& sh, const EncResult& res, int eo, int ro) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    uint32_t m = esc_nibbles(code[st]);
+    const uint32_t nw = nib[st];
     while (m) {
-      const int e = __builtin_ctz(m);
+      const int j4 = __builtin_ctz(m);  // 4 j
       m &= m - 1;
-      const uint32_t nib = (nw >> (4 * e)) & 0xFu;
-      const int word = bitpos >> 5;
-      if (word != acc_word) {
-        if (acc) atomicOr(&sh.var32[acc_word], acc);
-        acc = 0;
-        acc_word = word;
+      const uint32_t nv = (nw >> j4) & 0xFu;
+      sh.esc[eo] = (uint8_t)nv;
+      if (nv == (uint32_t)kRawNibble) {
+        // high byte of scalar j: byte 2 (j & 1) + 1 of dword j >> 1
+        const int j = j4 >> 2;
+        const uint32_t d = u4(wd[st], j >> 1);
+        const uint32_t hb = (d >> (8 + 16 * (j & 1))) & 0xFFu;
+        sh.var32[(res.raw_offset >> 2) + ro++] = (uint32_t)eo | (hb << 16);
       }
-      acc |= nib << (bitpos & 31);
-      if (nib == (uint32_t)kRawNibble) {
-        const uint4 wv = wd[st];
-        // high byte of scalar e (bytes 1, 3 of each dword)
-        const uint32_t hb = e < 4 ? perm(wv.y, wv.x, 0x07050301u) : perm(wv.w, wv.z, 0x07050301u);
-        sh.var32[(res.raw_offset >> 2) + ro++] = (uint32_t)eo | (((hb >> (8 * (e & 3))) & 0xffu) << 16);
-      }
-      bitpos += 4;
       ++eo;
     }
-  });
-  if (acc) atomicOr(&sh.var32[acc_word], acc);
+  }
   if (threadIdx.x == 0) {
     sh.var32[0] = res.etot;
     sh.var32[1] = res.rtot;
@@ -430,6 +446,19 @@ __device__ __forceinline__ void enc_var(const uint4 (&wd)[8], const uint32_t (&e
       rp += sh.wsum[1][w];
     }
   }
+  lds_barrier();
+  // pack: region dword 12 + k holds escape ordinals 8k .. 8k + 7 (nibble 2i
+  // low, 2i + 1 high in byte i); ordinals past etot are zero
+  for (int k = tid; 8 * k < res.etot; k += kThreads) {
+    const uint2 b = *reinterpret_cast<const uint2*>(sh.esc + 8 * k);
+    const int left = res.etot - 8 * k;  // > 0
+    const uint32_t keep_lo = left >= 4 ? 0xFFFFFFFFu : (1u << (8 * left)) - 1u;
+    const uint32_t keep_hi = left >= 8 ? 0xFFFFFFFFu : left <= 4 ? 0u : (1u << (8 * (left - 4))) - 1u;
+    const uint32_t lo = b.x & keep_lo, hi = b.y & keep_hi;
+    const uint32_t ev = perm(hi, lo, 0x06040200u), od = perm(hi, lo, 0x07050301u);
+    sh.var32[(kHeaderBytes >> 2) + k] = ev | (od << 4);
+  }
+  lds_barrier();
 }
 
 // Writes a coded record (dense part from registers, variable part from LDS)
@@ -484,11 +513,13 @@ __device__ __forceinline__ const uint8_t* record_src(const Store& s, int layer, 
 }
 
 #ifdef FP_TRACE_ENC
+// Optional per-workgroup phase sums (built only with -DFP_TRACE_ENC): slot k
+// accumulates s_memrealtime (100 MHz) at trace point k in registers over the
+// workgroup's records; written once at the end.
 __device__ uint64_t fp_enc_trace[1024 * 16];
-#define ENC_STAMP(k)                                                              \
-  do {                                                                            \
-    if (threadIdx.x == 0 && blockIdx.x < 1024 && r < 64 * (int)gridDim.x)       \
-      fp_enc_trace[blockIdx.x * 16 + (k)] += __builtin_amdgcn_s_memrealtime();   \
+#define ENC_STAMP(k)                                        \
+  do {                                                      \
+    enc_tacc[(k)] += __builtin_amdgcn_s_memrealtime();      \
   } while (0)
 #else
 #define ENC_STAMP(k) \
@@ -525,13 +556,19 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     heir2 = s.close_list[s.cap + (r + 2 * g) % n_closes];
   }
   int rank_kvh = -1;
+  // counter increments of this workgroup (thread 0), added once at the end:
+  // one hot counter hit by every record serialises at its memory channel
+  int n_enc = 0, n_fall = 0, n_err = 0, n_spill = 0;
+#ifdef FP_TRACE_ENC
+  uint64_t enc_tacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
   for (; r < n_rec; r += g) {
     const int kvh = r / n_closes;
     ENC_STAMP(0);
     const int64_t idx = ((int64_t)layer * s.NB + b) * per + kvh;
     int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
     if (kvh != rank_kvh) {  // consecutive records mostly share (layer, kvh)
-      sh.rank[tid] = rank_of[((int64_t)layer * per + kvh) * 256 + tid];
+      sh.tb[tid] = table_byte(rank_of[((int64_t)layer * per + kvh) * 256 + tid]);
       rank_kvh = kvh;
     }
     for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
@@ -565,18 +602,16 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     }
     lds_barrier();
     ENC_STAMP(2);
-    uint32_t sym[6];
-    uint64_t emask, rmask;
+    uint32_t sym[6], code[8], nib[8];
     int eo, ro;
-    uint32_t en[8];
-    const EncResult res = enc_analyse(wd, sh, sym, en, emask, rmask, eo, ro);
+    const EncResult res = enc_analyse(wd, sh, sym, code, nib, eo, ro);
     ENC_STAMP(3);
     if (res.codes) {
       // first claim attempt in flight while the variable region is built
       const int need = kDenseBytes + res.var_len;
       int prev = -1;
       if (tid == 0 && cur + need <= page_bytes) prev = atomicCAS(fill, cur, cur + need);
-      enc_var(wd, en, sh, res, emask, eo, ro);
+      enc_var(wd, code, nib, sh, res, eo, ro);
       ENC_STAMP(4);
       if (tid == 0) {
         int off = -1;
@@ -595,7 +630,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
             }
           }
         }
-        if (off < 0) atomicAdd(&s.counters[kSpills], 1);
+        n_spill += off < 0;
         sh.s_off = off;
       }
     } else if (tid == 0) {
@@ -607,9 +642,9 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       if (tid < 64) {
         const int slot = ovf_alloc_wave(s, (uint32_t)(b * per + kvh), tid);
         if (tid == 0) {
-          if (slot < 0) atomicAdd(&s.counters[kErrOverflow], 1);
-          atomicAdd(&s.counters[kFallbacks], 1);
-          atomicAdd(&s.counters[kEncoded], 1);
+          n_err += slot < 0;
+          ++n_fall;
+          ++n_enc;
           sh.s_ovf = slot;
         }
       }
@@ -630,7 +665,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       if (tid == 0) {
         s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
         s.rec_len[idx] = res.var_len;
-        atomicAdd(&s.counters[kEncoded], 1);
+        ++n_enc;
       }
     }
     ENC_STAMP(6);
@@ -645,6 +680,16 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     b2 = b3;
     heir2 = heir3;
   }
+  if (tid == 0) {
+    if (n_enc) atomicAdd(&s.counters[kEncoded], n_enc);
+    if (n_fall) atomicAdd(&s.counters[kFallbacks], n_fall);
+    if (n_err) atomicAdd(&s.counters[kErrOverflow], n_err);
+    if (n_spill) atomicAdd(&s.counters[kSpills], n_spill);
+  }
+#ifdef FP_TRACE_ENC
+  if (threadIdx.x == 0 && blockIdx.x < 1024)
+    for (int k = 0; k < 8; ++k) fp_enc_trace[blockIdx.x * 16 + k] = enc_tacc[k];
+#endif
 }
 
 // Closed blocks release their staging or pass it to their heir; the close
@@ -764,7 +809,7 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
   const int i = blockIdx.x, tid = threadIdx.x;
   const int kv = kvs[i];
   const uint16_t* src = raw + (int64_t)i * kTokens * kDim;
-  sh.rank[tid] = rank_of[(int64_t)tab_idx[i] * 256 + tid];
+  sh.tb[tid] = table_byte(rank_of[(int64_t)tab_idx[i] * 256 + tid]);
   for (int x = tid; x < kVarCap / 4; x += kThreads) sh.var32[x] = 0;
   // thread tid's kernel-order words from the token-major record
   const int w = tid >> 5, g = (tid >> 2) & 7, c = tid & 3;
@@ -785,11 +830,9 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
     wd[st] = make_uint4(d[0], d[1], d[2], d[3]);
   }
   __syncthreads();
-  uint32_t sym[6];
-  uint64_t emask, rmask;
+  uint32_t sym[6], code[8], nib[8];
   int eo, ro;
-  uint32_t en[8];
-  const EncResult res = enc_analyse(wd, sh, sym, en, emask, rmask, eo, ro);
+  const EncResult res = enc_analyse(wd, sh, sym, code, nib, eo, ro);
   uint8_t* dst = out + (int64_t)i * kRawRecord;
   if (!res.codes) {
 #pragma unroll
@@ -797,8 +840,7 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
     if (tid == 0) lens[i] = kRawRecord;
     return;
   }
-  enc_var(wd, en, sh, res, emask, eo, ro);
-  __syncthreads();
+  enc_var(wd, code, nib, sh, res, eo, ro);
   enc_store(dst, wd, sym, sh, res.var_len);
   if (tid == 0) lens[i] = kDenseBytes + res.var_len;
 }
