@@ -46,6 +46,7 @@ constexpr int kVRow = 136;         // LDS bytes per V^T row (128 + 8 pad)
 constexpr int kKBytes = kPfKeys * kKRow;   // 17408
 constexpr int kVBytes = kPfDim * kVRow;    // 17408
 constexpr int kStageBytes = kKBytes + kVBytes;
+constexpr float kLazyMax = 8.f;  // log2 headroom of the softmax reference max
 
 struct PrefillParams {
   const uint16_t* q;
@@ -85,24 +86,36 @@ struct TileRegs {
   uint4 v[4];
 };
 
-__device__ __forceinline__ const uint16_t* key_row(const PrefillParams& p, const int32_t* bt, int key, int h,
-                                                   const uint16_t* base) {
-  const int64_t page = bt[key >> 7];
-  return base + ((page * 128 + (key & 127)) * p.kvh + h) * kPfDim;
+typedef __amdgpu_buffer_rsrc_t pf_rsrc_t;
+typedef uint32_t pf_u32x4 __attribute__((ext_vector_type(4)));
+
+// A 64-key tile lies in one 128-token page (tiles start at multiples of 64):
+// rows key0 .. key0 + nkeys - 1 of head h are ``row`` bytes apart from the
+// tile's first row; a buffer resource over exactly those rows reads zero
+// past them.
+__device__ __forceinline__ pf_rsrc_t tile_rsrc(const uint16_t* base, int64_t page, int key0, int nkeys, int h,
+                                               int kvh) {
+  const uint16_t* first = base + ((page * 128 + (key0 & 127)) * kvh + h) * kPfDim;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(first), (short)0, nkeys * kvh * kPfDim * 2,
+                                           0x00020000);
 }
 
-__device__ __forceinline__ void load_tile(const PrefillParams& p, const int32_t* bt, int key0, int nkeys, int h,
+__device__ __forceinline__ uint4 pf_bld16(pf_rsrc_t r, int off) {
+  const pf_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void load_tile(const PrefillParams& p, int64_t page, int key0, int nkeys, int h,
                                           TileRegs& r) {
   const int t = threadIdx.x;
   const int dc = t & 15;
+  const int row = p.kvh * kPfDim * 2;  // bytes between consecutive keys
+  const pf_rsrc_t rk = tile_rsrc(p.wk, page, key0, nkeys, h, p.kvh);
+  const pf_rsrc_t rv = tile_rsrc(p.wv, page, key0, nkeys, h, p.kvh);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int kk = 16 * i + (t >> 4);
-    r.k[i] = kk < nkeys ? *reinterpret_cast<const uint4*>(key_row(p, bt, key0 + kk, h, p.wk) + 8 * dc)
-                        : make_uint4(0u, 0u, 0u, 0u);
-    const int kv = 4 * (t >> 4) + i;
-    r.v[i] = kv < nkeys ? *reinterpret_cast<const uint4*>(key_row(p, bt, key0 + kv, h, p.wv) + 8 * dc)
-                        : make_uint4(0u, 0u, 0u, 0u);
+    r.k[i] = pf_bld16(rk, (16 * i + (t >> 4)) * row + 16 * dc);
+    r.v[i] = pf_bld16(rv, (4 * (t >> 4) + i) * row + 16 * dc);
   }
 }
 
@@ -180,9 +193,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) o[dt][qt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // page ids of the tiles: lane j holds block_table entry 64 pb + j
+  int pages = 0, pbase = -1;
+  auto page_of = [&](int key0) -> int64_t {
+    const int pi = key0 >> 7;
+    if ((pi & ~63) != pbase) {
+      pbase = pi & ~63;
+      pages = pbase + lane < (kend + 127) / 128 ? bt[pbase + lane] : 0;
+    }
+    return __builtin_amdgcn_readlane(pages, pi & 63);
+  };
   TileRegs regs;
   if (ntiles > 0) {
-    load_tile(p, bt, 0, min(kPfKeys, kend), h, regs);
+    load_tile(p, page_of(0), 0, min(kPfKeys, kend), h, regs);
     store_tile(pf_smem, regs);
   }
   __syncthreads();
@@ -190,7 +213,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
     const int key0 = it * kPfKeys;
     const uint8_t* stage = pf_smem + (it & 1) * kStageBytes;
     const bool more = it + 1 < ntiles;
-    if (more) load_tile(p, bt, key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, regs);
+    if (more) load_tile(p, page_of(key0 + kPfKeys), key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, regs);
 
     // ---- S^T = K Q^T: s[kt][qt], keys key0 + 16 kt + 4 q4 + r ----
     pf_f32x4 s[4][2];
@@ -206,38 +229,54 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
       }
     }
     // ---- mask, online softmax, P^T fragments ----
+    // Scores stay unscaled (scale > 0 keeps the order); P = exp2(s c - m c)
+    // is one FMA and one exp per score.  The reference max m only moves when
+    // some column's max outgrows it by more than 2^kLazyMax (log2 domain), so
+    // O and l are rescaled on few tiles; P <= 2^kLazyMax is exact enough in
+    // BF16 and fp32.
     const bool edge = key0 + kPfKeys > min(kmax[0], kmax[1]);  // wave-uniform enough; exact test below
-    uint4 pf[2][2];  // [kk][qt]
+    float mloc[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      float mloc = -INFINITY;
+      float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float x = s[kt][qt][r] * p.scale_log2;
-          if (edge && key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) x = -INFINITY;
-          s[kt][qt][r] = x;
-          mloc = fmaxf(mloc, x);
+          if (edge && key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) s[kt][qt][r] = -INFINITY;
+          mx = fmaxf(mx, s[kt][qt][r]);
         }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m[qt], mloc);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
-      m[qt] = m_new;
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mloc[qt] = mx;
+    }
+    const bool grow = (mloc[0] > m[0] && (m[0] == -INFINITY || (mloc[0] - m[0]) * p.scale_log2 > kLazyMax)) ||
+                      (mloc[1] > m[1] && (m[1] == -INFINITY || (mloc[1] - m[1]) * p.scale_log2 > kLazyMax));
+    if (__ballot(grow) != 0) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float m_new = fmaxf(m[qt], mloc[qt]);
+        const float alpha = m[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m[qt] - m_new) * p.scale_log2);
+        m[qt] = m_new;
+        l[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+      }
+    }
+    uint4 pf[2][2];  // [kk][qt]
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float nm = m[qt] == -INFINITY ? 0.f : -m[qt] * p.scale_log2;
       float psum = 0.f;
       float e[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          e[kt][r] = __builtin_amdgcn_exp2f(s[kt][qt][r] - m_use);
+          e[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, nm));
           psum += e[kt][r];
         }
-      l[qt] = l[qt] * alpha + psum;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+      l[qt] += psum;
       // B operand of k-step kk: keys 32 kk + {4 q4 .. 4 q4 + 3} (tile 2 kk) and
       // 32 kk + 16 + {4 q4 ..} (tile 2 kk + 1)
 #pragma unroll

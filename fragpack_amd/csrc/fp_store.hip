@@ -537,24 +537,31 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   const int n_rec = n_closes * per;
   int r = blockIdx.x;
   if (r >= n_rec) return;
-  // Record metadata runs ahead of the data: at record r the stage streams
-  // record r + grid (address known since the previous record), the slot of
-  // r + 2 grid is read and the close entry of r + 3 grid.
+  // Record metadata (block, heir, staging slot) of this workgroup's records
+  // in batches of 64 (record r + j grid in lane j), loaded with vector loads
+  // one batch ahead: scalar loads would be waited for at every LDS barrier.
+  // The stage streams record r + grid while r is encoded.
   const int g = (int)gridDim.x;
-  int b = s.close_list[r % n_closes];
-  int heir = s.close_list[s.cap + r % n_closes];
-  uint8_t* src = staging_addr(s, s.wslot[b], layer, r / n_closes);
+  const int lane = tid & 63;
+  auto load_meta = [&](int k0, int& mb, int& mh, int& mw) {
+    mb = 0;
+    mh = -1;
+    mw = 0;
+    const int rr = (int)blockIdx.x + (k0 + lane) * g;
+    if (rr < n_rec) {
+      const int ci = rr % n_closes;
+      mb = s.close_list[ci];
+      mh = s.close_list[s.cap + ci];
+      mw = s.wslot[mb];
+    }
+  };
+  int cb, ch, cw, nb, nh, nw;  // current / next batch
+  load_meta(0, cb, ch, cw);
+  load_meta(64, nb, nh, nw);
+  int b = __builtin_amdgcn_readfirstlane(cb);
+  int heir = __builtin_amdgcn_readfirstlane(ch);
+  uint8_t* src = staging_addr(s, __builtin_amdgcn_readfirstlane(cw), layer, r / n_closes);
   stage_record(stage, src);
-  int b1 = 0, heir1 = -1, w1 = 0, b2 = 0, heir2 = -1;
-  if (r + g < n_rec) {
-    b1 = s.close_list[(r + g) % n_closes];
-    heir1 = s.close_list[s.cap + (r + g) % n_closes];
-    w1 = s.wslot[b1];
-  }
-  if (r + 2 * g < n_rec) {
-    b2 = s.close_list[(r + 2 * g) % n_closes];
-    heir2 = s.close_list[s.cap + (r + 2 * g) % n_closes];
-  }
   int rank_kvh = -1;
   // counter increments of this workgroup (thread 0), added once at the end:
   // one hot counter hit by every record serialises at its memory channel
@@ -562,7 +569,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
 #ifdef FP_TRACE_ENC
   uint64_t enc_tacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #endif
-  for (; r < n_rec; r += g) {
+  for (int k = 0; r < n_rec; r += g, ++k) {
     const int kvh = r / n_closes;
     ENC_STAMP(0);
     const int64_t idx = ((int64_t)layer * s.NB + b) * per + kvh;
@@ -582,16 +589,22 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     for (int st = 0; st < 8; ++st) wd[st] = stage.w[st][tid];
     __builtin_amdgcn_s_waitcnt(0);  // reads done before the stage is refilled
     ENC_STAMP(1);
+    // the next record's metadata: lane (k + 1) % 64 of the current or next batch
+    const int k1 = (k + 1) & 63;
+    const bool nbatch = k1 == 0;
+    const int b1 = __builtin_amdgcn_readlane(nbatch ? nb : cb, k1);
+    const int heir1 = __builtin_amdgcn_readlane(nbatch ? nh : ch, k1);
+    const int w1 = __builtin_amdgcn_readlane(nbatch ? nw : cw, k1);
     uint8_t* src1 = src;
     if (r + g < n_rec) {
       src1 = staging_addr(s, w1, layer, (r + g) / n_closes);
       stage_record(stage, src1);
     }
-    int w2 = 0, b3 = 0, heir3 = -1;
-    if (r + 2 * g < n_rec) w2 = s.wslot[b2];
-    if (r + 3 * g < n_rec) {
-      b3 = s.close_list[(r + 3 * g) % n_closes];
-      heir3 = s.close_list[s.cap + (r + 3 * g) % n_closes];
+    if (nbatch) {  // the next batch becomes current; load the one after
+      cb = nb;
+      ch = nh;
+      cw = nw;
+      load_meta(k + 65, nb, nh, nw);
     }
     if (heir >= 0) {
       const uint8_t* from = staging_addr(s, s.wslot[heir], layer, kvh);
@@ -674,11 +687,6 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     b = b1;
     heir = heir1;
     src = src1;
-    b1 = b2;
-    heir1 = heir2;
-    w1 = w2;
-    b2 = b3;
-    heir2 = heir3;
   }
   if (tid == 0) {
     if (n_enc) atomicAdd(&s.counters[kEncoded], n_enc);
