@@ -44,9 +44,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 
-#ifndef FP_DECODE_BATCHED
-#define FP_DECODE_BATCHED 1
-#endif
 #ifndef FP_PERSIST
 #define FP_PERSIST 1
 #endif
@@ -396,9 +393,7 @@ __device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, in
 
 // Decodes this lane's kernel-order thread ``nt`` of the wave's slab ``w`` of
 // record ``r`` (escapes staged in ``esc``, header in ``hdr``) and calls
-// pair(a, word 2a, word 2a + 1, fragment a of ``tile``) for a = 0..3.  The
-// four B fragments are read from ``tile`` in the same LDS batch as the
-// escape windows.
+// pair(a, word 2a, word 2a + 1, fragment a of ``tile``) for a = 0..3.
 template <typename Pair>
 __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int w, int nt, NatPerm np,
                                             const HeadLut& lut, const uint8_t* esc, const uint32_t* hdr,
@@ -420,11 +415,7 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
   }
   const int e0 = (int)(hdr[4 + w] & 0xFFFFu);  // esc_prefix[2 w]
   const int excl = natural_prefix(thread_escapes(b), np);
-#if FP_DECODE_BATCHED
-  decode_words_batched(b, esc, e0 + excl, lut.p0, lut.p1, emit);
-#else
   decode_words(b, esc, e0 + excl, lut.p0, lut.p1, emit);
-#endif
 }
 
 // Optional per-workgroup timeline (built only with -DFP_TRACE): slot k of

@@ -335,49 +335,6 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
   });
 }
 
-// decode_words with every LDS access issued up front: the eight escape
-// windows (12 bytes each, at the 4-aligned address below the word's first
-// escape) are read in one batch, so a lane waits for LDS once per thread
-// instead of once per word.  Same output as decode_words.
-template <typename Emit>
-__device__ __forceinline__ void decode_words_batched(const SlabBuf& b, const uint8_t* esc, int eo, uint32_t lut0,
-                                                     uint32_t lut1, Emit&& emit) {
-  uint32_t sk[8], win[8][3];
-  int sh[8];
-  static_for<0, 8>([&](auto st_c) {
-    constexpr int st = decltype(st_c)::value;
-    sk[st] = sym_word(b, st);
-    const uint32_t* ew = reinterpret_cast<const uint32_t*>(esc + (eo & ~3));
-    win[st][0] = ew[0];
-    win[st][1] = ew[1];
-    win[st][2] = ew[2];
-    sh[st] = eo & 3;
-    eo += __builtin_popcount((sk[st] + 0x11111111u) & 0x88888888u);
-  });
-  asm volatile("" ::: "memory");  // keep the window reads ahead of their uses
-  static_for<0, 8>([&](auto st_c) {
-    constexpr int st = decltype(st_c)::value;
-    const uint32_t s = sk[st];
-    const uint32_t b8 = (s + 0x11111111u) & 0x88888888u;
-    const uint32_t eb = b8 >> 3;
-    const uint32_t hp_ev = perm(lut1, lut0, s & 0x07070707u);
-    const uint32_t hp_od = perm(lut1, lut0, (s >> 4) & 0x07070707u);
-    const uint32_t elo = alignbyte(win[st][1], win[st][0], (uint32_t)sh[st]);
-    const uint32_t ehi = alignbyte(win[st][2], win[st][1], (uint32_t)sh[st]);
-    const uint32_t rank = eb * 0x11111110u;
-    const uint32_t m15 = b8 | (b8 - eb);
-    const uint32_t sel = (rank & m15) | (~m15 & 0xCCCCCCCCu);
-    const uint32_t h_ev = hp_ev | perm(ehi, elo, sel & 0x0F0F0F0Fu);
-    const uint32_t h_od = hp_od | perm(ehi, elo, (sel >> 4) & 0x0F0F0F0Fu);
-    const uint32_t h01 = perm(h_od, h_ev, 0x05010400u);
-    const uint32_t h23 = perm(h_od, h_ev, 0x07030602u);
-    const uint4 lw = b.v[st >> 1];
-    const uint32_t la = (st & 1) ? lw.z : lw.x, lb = (st & 1) ? lw.w : lw.y;
-    emit(st_c, make_uint4(perm(h01, la, 0x05010400u), perm(h01, la, 0x07030602u), perm(h23, lb, 0x05010400u),
-                          perm(h23, lb, 0x07030602u)));
-  });
-}
-
 // Escape count of one thread's 64 scalars.
 __device__ __forceinline__ int thread_escapes(const SlabBuf& b) {
   int n = 0;
