@@ -326,8 +326,13 @@ def encode_bench(torch, args) -> dict:
     ms = total / reps
     c = store.counters.cpu().numpy()
     rec_len = store.rec_len[0].cpu().numpy()
+    addr = store.rec_addr[0].cpu().numpy()
     coded = rec_len <= 2048
-    written = int(np.where(coded, DENSE + rec_len, 32768).sum())
+    # records that fell back were written raw to the overflow pool, unless it
+    # was full (then they stay in staging and nothing is written)
+    o0 = store.overflow.data_ptr()
+    in_ovf = (addr >= o0) & (addr < o0 + store.overflow.numel())
+    written = int((DENSE + rec_len[coded]).sum()) + 32768 * int((in_ovf & ~coded).sum())
     records = n * 2 * H
     eff = records * 32768
     log(f"encode: {records} records in {ms * 1e3:.0f} us -> {eff / ms / 1e6:.0f} GB/s effective, "

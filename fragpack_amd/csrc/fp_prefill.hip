@@ -42,7 +42,11 @@ constexpr int kPfRows = 128;       // query rows (token x head) per workgroup
 constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfDim = 128;
 constexpr int kKRow = 272;         // LDS bytes per K row (256 + 16 pad)
-constexpr int kVRow = 136;         // LDS bytes per V^T row (128 + 8 pad)
+// V^T rows of 144 bytes with the 8-byte key blocks of row d stored at block
+// index kb ^ ((d >> 3) & 15): both the transposing writes and the fragment
+// reads then spread over all banks (unswizzled 136-byte rows put eight lanes
+// of every transposing write on the same banks).
+constexpr int kVRow = 144;
 constexpr int kKBytes = kPfKeys * kKRow;   // 17408
 constexpr int kVBytes = kPfDim * kVRow;    // 17408
 constexpr int kStageBytes = kKBytes + kVBytes;
@@ -136,8 +140,9 @@ __device__ __forceinline__ void store_tile(uint8_t* stage, const TileRegs& r) {
     // dims 8 dc + 2e (low halves) and 8 dc + 2e + 1 (high halves)
     const uint2 lo = make_uint2(pf_perm(b, a, 0x05040100u), pf_perm(d, c, 0x05040100u));
     const uint2 hi = make_uint2(pf_perm(b, a, 0x07060302u), pf_perm(d, c, 0x07060302u));
-    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e) * kVRow + 8 * kg) = lo;
-    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e + 1) * kVRow + 8 * kg) = hi;
+    // rows 8 dc + 2 e (+ 1): (d >> 3) & 15 = dc
+    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e) * kVRow + 8 * (kg ^ dc)) = lo;
+    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e + 1) * kVRow + 8 * (kg ^ dc)) = hi;
   }
 }
 
@@ -289,10 +294,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const uint8_t* vrow = vt + (16 * dt + j) * kVRow;
+      const int sw = (2 * dt + (j >> 3)) & 15;  // (row >> 3) & 15
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 2 * (32 * kk + 4 * q4));
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 2 * (32 * kk + 16 + 4 * q4));
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 8 * ((8 * kk + q4) ^ sw));
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8 * ((8 * kk + 4 + q4) ^ sw));
         const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
         o[dt][0] = pf_mfma(vf, pf[kk][0], o[dt][0]);
         o[dt][1] = pf_mfma(vf, pf[kk][1], o[dt][1]);
