@@ -239,7 +239,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
     // some column's max outgrows it by more than 2^kLazyMax (log2 domain), so
     // O and l are rescaled on few tiles; P <= 2^kLazyMax is exact enough in
     // BF16 and fp32.
-    const bool edge = key0 + kPfKeys > min(kmax[0], kmax[1]);  // wave-uniform enough; exact test below
+    // causal / length mask: only on tiles that reach some column's limit
+    // (a wave-uniform branch; other tiles skip the compares)
+    if (__ballot(key0 + kPfKeys > min(kmax[0], kmax[1])) != 0) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) s[kt][qt][r] = -INFINITY;
+    }
     float mloc[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -247,10 +257,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (edge && key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) s[kt][qt][r] = -INFINITY;
-          mx = fmaxf(mx, s[kt][qt][r]);
-        }
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       mloc[qt] = mx;
