@@ -680,7 +680,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         }
       }
     }
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;  // m_run: unscaled score units
+    const float lazy = kLazyMax / p.scale_log2;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
     FP_STAMP(2);
     expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
@@ -715,30 +716,37 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                     s1 = mfma(a_frag(w0, w1, 1), qa, s1);
                   });
       // token of s_j[r] = 32 w + 16 (c >> 1) + 8 j + 4 (c & 1) + r
-      const int tb = tok0 + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
+      // Scores stay unscaled (scale > 0 keeps their order; P = exp2(s c - m c)
+      // is one FMA and one exp); the page past the context is masked in a
+      // wave-uniform branch.
+      if (tok0 + kTokens > seq) {
+        const int tb = tok0 + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (tb + r >= seq) s0[r] = -INFINITY;
+          if (tb + 8 + r >= seq) s1[r] = -INFINITY;
+        }
+      }
       float mloc = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s0[r] = tb + r < seq ? s0[r] * p.scale_log2 : -INFINITY;
-        s1[r] = tb + 8 + r < seq ? s1[r] * p.scale_log2 : -INFINITY;
-        mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
-      }
+      for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
       if (lane < 8) sh.red[w][lane] = mloc;
       // Softmax against the running max m_run, speculatively: the page max is
-      // known only after the barrier.  P = exp2(s - m_run) stays exact while
-      // the page max exceeds m_run by at most kLazyMax (P <= 2^kLazyMax);
+      // known only after the barrier.  P = exp2((s - m_run) c) stays exact
+      // while the page max exceeds m_run by at most kLazyMax / c (P <= 2^kLazyMax);
       // otherwise (and on the first page) P is recomputed below with a new
       // reference max, at the cost of one more barrier.
       float e0[4], e1[4], psum = 0.f;
       const bool spec = m_run != -INFINITY;  // the same in every wave
       auto softmax_tile = [&](float m_ref) {
         psum = 0.f;
+        const float nm = -m_ref * p.scale_log2;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          e0[r] = __builtin_amdgcn_exp2f(s0[r] - m_ref);
-          e1[r] = __builtin_amdgcn_exp2f(s1[r] - m_ref);
+          e0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], p.scale_log2, nm));
+          e1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], p.scale_log2, nm));
           psum += e0[r] + e1[r];
         }
         // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
@@ -765,10 +773,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       FP_STAMP(5 + 5 * min(i, 4));
       const float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
       // the same decision in every wave: all read the same page maxima
-      if (!spec || __ballot(mpage > m_run + kLazyMax) != 0) {
+      if (!spec || __ballot(mpage > m_run + lazy) != 0) {
         const float m_new = fmaxf(m_run, mpage);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.scale_log2);
         m_run = m_new;
         l_run *= alpha;
         o0 *= alpha;
@@ -823,7 +831,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       const int64_t i0 = row * kDim + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
       st_coh4(ro, i0, o0[0], o0[1], o0[2], o0[3]);
       st_coh4(ro, i0 + 8, o1[0], o1[1], o1[2], o1[3]);
-      if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run, l_all);
+      if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run * p.scale_log2, l_all);
     }
     FP_STAMP(28);
     merge_chunks(p, sh, b, h, first, chunks);
@@ -873,6 +881,7 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
                                int64_t units, int replan, double scale, fp_stream_t stream) {
   FP_CHECK(batch >= 0 && kv_heads > 0, "decode needs batch >= 0 and kv_heads > 0");
   FP_CHECK(group == 1 || group == 2 || group == 4 || group == 8, "query heads need a group dividing 8");
+  FP_CHECK(scale > 0, "softmax scale must be positive");
   if (batch == 0) return 0;
   FP_CHECK(units >= batch, "decode needs at least one unit per sequence");
   FP_CHECK(q_stride % 8 == 0 && q_stride >= kv_heads * group * kDim && reinterpret_cast<uintptr_t>(q) % 16 == 0,
