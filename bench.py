@@ -427,8 +427,9 @@ def main() -> None:
         print(json.dumps({"copy_bytes": 4 << 28, "copies": 3}))
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus N > 1 is not supported (see DESIGN.md, "
-                                   "'How the path would shard')"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus N > 1 is not supported (the path would "
+                                   "shard by KV head or by sequence with no exchange; only one GPU's share is "
+                                   "built and measured)"}))
         sys.exit(2)
     import torch
 
