@@ -1,0 +1,190 @@
+"""The BASELINE configs at their full sizes on the GPU path.
+
+Small parity cases live in the other test files; these run each config's real
+shape through the store and kernels and check what the sizes allow:
+- config 1 (B4 x H4 x G8 x 8192) and config 2 (MHA, B16 x H32, ragged
+  U[129, 4096], 5% outlier channels): decode attention vs a float64 softmax
+  over the same KV, records built by the CPU oracle, 2e-2 abs + 1e-2 rel;
+- config 3 (32768 blocks x 8 heads x K/V, 10% Student-t(2) x 16, 8192-record
+  overflow pool): encode -> gather is bit-exact for all 524,288 records, the
+  store counters agree with the records' placement, and sampled coded and
+  fallback records are byte-identical to the oracle codec;
+- config 4 decode (B64 x H8 x G4 x 32768): sampled sequences vs fp32
+  attention over the written KV; config 4 prefill (4 x 8192 causal, Hq 32 /
+  H 8): sampled query rows vs fp32.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from tests import kvgen, workloads
+from tests.conftest import gpu_available
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
+
+ATOL, RTOL = 2e-2, 1e-2
+T, D = 128, 128
+
+
+def _decode_vs_float64(case):
+    out = kvgen.run_gpu_decode(case)
+    ref = kvgen.reference_attention(case)
+    assert np.all(np.isfinite(out))
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_config1_full_size():
+    case = kvgen.decode_case(seed=101, batch=4, heads=4, group=8, lens=[8192] * 4, outlier=0.02)
+    print("config1 case built", flush=True)
+    _decode_vs_float64(case)
+
+
+def test_config2_mha_ragged():
+    rng = np.random.default_rng(102)
+    lens = rng.integers(129, 4097, 16).astype(np.int32)
+    case = kvgen.decode_case(seed=102, batch=16, heads=32, group=1, lens=lens, outlier=0.05)
+    print("config2 case built", list(lens), flush=True)
+    _decode_vs_float64(case)
+
+
+def test_config3_encoder_full_size():
+    import torch
+
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops import hbm_kv
+    from fragpack_amd.ops.hbm_kv import RAW_VAR_LEN, HbmKvStore, StoreError, page_bytes
+
+    H, n, cap = 8, 32768, 8192
+    rng = np.random.default_rng(103)
+    scales = workloads.channel_scales(rng, H, 0.02)
+    tables = workloads.calibrated_tables(rng, H, scales)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(103)
+    scales_t = torch.from_numpy(scales).float().to(dev)
+    arena = torch.empty((n, page_bytes(H)), dtype=torch.uint8, device=dev)
+    store = HbmKvStore([arena], H, device_tables(tables, dev), max_tokens=n * T, staging_slots=1,
+                       overflow_records=cap)
+    slots = torch.arange(n * T, device=dev, dtype=torch.int64)
+    store.prepare(slots, slots.numel(), np.zeros(0, np.int32))
+    kv = torch.empty((2, n * T, H, D), dtype=torch.bfloat16, device=dev)
+    chunk = 2048 * T
+    for t0 in range(0, n * T, chunk):
+        kv[:, t0 : t0 + chunk] = workloads.gen_kv(torch, gen, chunk, H, scales_t, heavy=0.1)
+        store.write(0, kv[0, t0 : t0 + chunk], kv[1, t0 : t0 + chunk], slots[t0 : t0 + chunk])
+    print("config3 written", flush=True)
+    store.encode(0, n)
+    torch.cuda.synchronize()
+    # the full pool drops records (they stay in staging): stats() reports the loss
+    with pytest.raises(StoreError):
+        store.stats()
+    c = store.counters.cpu().numpy()
+    encoded, fallbacks, err_overflow, spills = (int(c[i]) for i in (hbm_kv._ENCODED, hbm_kv._FALLBACKS,
+                                                                   hbm_kv._ERR_OVERFLOW, hbm_kv._SPILLS))
+    rec_len = store.rec_len[0].cpu().numpy()  # [n, 2, H]
+    raw = rec_len == RAW_VAR_LEN
+    print("config3 encoded", encoded, fallbacks, err_overflow, spills, flush=True)
+    assert encoded == n * 2 * H
+    assert fallbacks == int(raw.sum()) and fallbacks > cap
+    assert err_overflow == fallbacks - cap
+    assert spills == 0
+    assert np.all(rec_len[~raw] <= 2048) and np.all(rec_len[~raw] % 16 == 0)
+    # every record decodes back to the written KV, bit for bit
+    for b0 in range(0, n, 4096):
+        blocks = torch.arange(b0, b0 + 4096, dtype=torch.int32, device=dev)
+        wk = torch.empty((4096, T, H, D), dtype=torch.bfloat16, device=dev)
+        wv = torch.empty_like(wk)
+        store.gather(0, blocks, wk, wv)
+        ref = kv[:, b0 * T : (b0 + 4096) * T].view(2, 4096, T, H, D)
+        assert torch.equal(wk.view(torch.int16), ref[0].view(torch.int16))
+        assert torch.equal(wv.view(torch.int16), ref[1].view(torch.int16))
+    print("config3 gather bit-exact", flush=True)
+    # sampled records byte-identical to the oracle codec (coded) / raw form (fallback)
+    addr = store.rec_addr[0].cpu().numpy()
+    o0, a0 = store.overflow.data_ptr(), arena.data_ptr()
+    ovf = store.overflow.view(-1)
+    flat_arena = arena.view(-1)
+    coded = np.argwhere(~raw)
+    in_pool = np.argwhere(raw & (addr >= o0) & (addr < o0 + store.overflow.numel()))
+    picks = [tuple(x) for x in coded[rng.choice(len(coded), 24, replace=False)]]
+    picks += [tuple(x) for x in in_pool[rng.choice(len(in_pool), 8, replace=False)]]
+    host_tables = tables[0]
+    for b, k, h in picks:
+        tok = kv[k, b * T : (b + 1) * T, h].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        if raw[b, k, h]:
+            want = oracle.raw_record(tok, k)
+            got = ovf[addr[b, k, h] - o0 : addr[b, k, h] - o0 + len(want)].cpu().numpy().tobytes()
+        else:
+            want = oracle.encode_record(tok, host_tables[k, h], k)
+            got = flat_arena[addr[b, k, h] - a0 : addr[b, k, h] - a0 + len(want)].cpu().numpy().tobytes()
+            assert len(want) == 22528 + rec_len[b, k, h]
+        assert got == want, (b, k, h)
+
+
+def test_config4_decode_full_size():
+    import math
+
+    import torch
+
+    from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
+
+    B, H, G, ctx = 64, 8, 4, 32768
+    rng = np.random.default_rng(104)
+    scales = workloads.channel_scales(rng, H, 0.02)
+    tables = workloads.calibrated_tables(rng, H, scales)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(104)
+    scales_t = torch.from_numpy(scales).float().to(dev)
+    pages = math.ceil(ctx / T)
+    nb = B * pages
+    store, arena, kv = workloads.build_store(torch, H, nb, tables, gen, scales_t, fill_blocks=256, keep_kv=True)
+    print("config4 store built", store.stats(), flush=True)
+    bt = torch.from_numpy(rng.permutation(nb).astype(np.int32).reshape(B, pages)).to(dev)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    q = torch.randn((B, H * G, D), generator=gen, device=dev).to(torch.bfloat16)
+    units = decode_units(B, H, torch.cuda.get_device_properties(dev).multi_processor_count)
+    o, m, p = workspace_elems(H, units)
+    ws = (torch.empty(o, device=dev), torch.empty(m, device=dev), torch.empty(p, dtype=torch.int32, device=dev))
+    out = torch.full_like(q, float("nan"))
+    tabs = RecordTables(*store.layer_tables(0))
+    decode_attention(q, tabs, bt, lens, D ** -0.5, units, out, ws, True)  # planner launch (fresh workspace)
+    decode_attention(q, tabs, bt, lens, D ** -0.5, units, out, ws, True)  # plans inside the kernel
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    rows = np.sort(rng.choice(B, 6, replace=False))
+    ref = workloads.reference_decode(torch, q[rows], kv, bt.cpu()[rows], lens.cpu().numpy()[rows], H, G, D ** -0.5)
+    torch.testing.assert_close(out[rows].float(), ref, atol=ATOL, rtol=RTOL)
+
+
+def test_config4_prefill_full_size():
+    import torch
+
+    from fragpack_amd.ops.prefill_attn import flash_attn_varlen_func
+
+    S, L, H, G = 4, 8192, 8, 4
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(105)
+    rng = np.random.default_rng(105)
+    n_pages = S * (L // T)
+    bt = torch.from_numpy(rng.permutation(n_pages).astype(np.int32).reshape(S, L // T)).to(dev)
+    wk = torch.randn((n_pages, T, H, D), generator=gen, device=dev).to(torch.bfloat16)
+    wv = torch.randn((n_pages, T, H, D), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((S * L, H * G, D), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.full_like(q, float("nan"))
+    cu = torch.arange(0, S * L + 1, L, dtype=torch.int32, device=dev)
+    kl = torch.full((S,), L, dtype=torch.int32, device=dev)
+    flash_attn_varlen_func(q=q, k=wk, v=wv, out=out, cu_seqlens_q=cu, max_seqlen_q=L, seqused_k=kl, max_seqlen_k=L,
+                           softmax_scale=D ** -0.5, causal=True, block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for s in range(S):
+        rows = torch.from_numpy(np.sort(rng.choice(L, 32, replace=False))).to(dev)
+        pg = bt[s].long()
+        k = wk[pg].reshape(-1, H, D).float().repeat_interleave(G, dim=1)
+        v = wv[pg].reshape(-1, H, D).float().repeat_interleave(G, dim=1)
+        sc = torch.einsum("rhd,khd->hrk", q[s * L + rows].float(), k) * D ** -0.5
+        sc = sc.masked_fill(torch.arange(L, device=dev)[None, None, :] > rows[None, :, None], float("-inf"))
+        ref = torch.einsum("hrk,khd->rhd", torch.softmax(sc, -1), v)
+        torch.testing.assert_close(out[s * L + rows].float(), ref, atol=ATOL, rtol=RTOL)
