@@ -332,8 +332,11 @@ __device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt
 }
 
 // This lane's 8 bytes (at 512 w + 8 lane) of the record's variable region.
+// A wave whose quarter lies past the region (or a raw record) loads nothing.
+__device__ __forceinline__ bool quarter_used(const RecRef& r, int w) { return r.vlen <= kVarCap && 512 * w < r.vlen; }
+
 __device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane) {
-  return r.vlen > kVarCap ? make_uint2(0u, 0u) : bld8(r.rs, 8 * lane, kDenseBytes + 512 * w);
+  return quarter_used(r, w) ? bld8(r.rs, 8 * lane, kDenseBytes + 512 * w) : make_uint2(0u, 0u);
 }
 
 // Per-record escape staging, done by all four waves from their prefetched
@@ -342,7 +345,7 @@ __device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane) 
 // LDS; then, after a barrier, (2) raw-list entries patch their escapes.
 __device__ __forceinline__ void expand_var(const RecRef& r, uint2 v, int w, int lane, const uint32_t (&sl)[4],
                                            uint8_t* esc, uint32_t* hdr) {
-  if (r.vlen > kVarCap) return;
+  if (!quarter_used(r, w)) return;
   const int o = 512 * w + 8 * lane;
   if (o >= kHeaderBytes) {
     const uint2 e0 = expand_nibbles(v.x, sl), e1 = expand_nibbles(v.y, sl);
@@ -355,7 +358,7 @@ __device__ __forceinline__ void expand_var(const RecRef& r, uint2 v, int w, int 
 
 __device__ __forceinline__ void patch_raw(const RecRef& r, uint2 v, int w, int lane, uint8_t* esc,
                                           const uint32_t* hdr) {
-  if (r.vlen > kVarCap) return;
+  if (!quarter_used(r, w)) return;
   const int n_raw = (int)hdr[1], raw_offset = (int)hdr[2];
   const int o = 512 * w + 8 * lane;
 #pragma unroll

@@ -318,7 +318,8 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
     const int a = eo & ~3;
     const uint32_t* ew = reinterpret_cast<const uint32_t*>(esc + a);
     const uint32_t d0 = ew[0], d1 = ew[1], d2 = ew[2];
-    const uint32_t elo = alignbyte(d1, d0, (uint32_t)(eo & 3)), ehi = alignbyte(d2, d1, (uint32_t)(eo & 3));
+    // v_alignbyte_b32 shifts by 8 x bits [1:0] of its last operand: eo as is
+    const uint32_t elo = alignbyte(d1, d0, (uint32_t)eo), ehi = alignbyte(d2, d1, (uint32_t)eo);
     eo += __builtin_popcount(eb);
     // selector nibble: exclusive escape rank for escapes, 0xC (-> 0x00) else
     const uint32_t rank = eb * 0x11111110u;
