@@ -566,6 +566,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   // counter increments of this workgroup (thread 0), added once at the end:
   // one hot counter hit by every record serialises at its memory channel
   int n_enc = 0, n_fall = 0, n_err = 0, n_spill = 0;
+  bool ovf_full = false;  // this workgroup found the overflow pool full
 #ifdef FP_TRACE_ENC
   uint64_t enc_tacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #endif
@@ -653,7 +654,10 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     ENC_STAMP(5);
     if (sh.s_off < 0) {
       if (tid < 64) {
-        const int slot = ovf_alloc_wave(s, (uint32_t)(b * per + kvh), tid);
+        // Nothing frees overflow slots while an encode runs (frees happen in
+        // prepare, on the same stream), so once this workgroup finds the pool
+        // full every later allocation of the launch fails too: skip the scan.
+        const int slot = ovf_full ? -1 : ovf_alloc_wave(s, (uint32_t)(b * per + kvh), tid);
         if (tid == 0) {
           n_err += slot < 0;
           ++n_fall;
@@ -663,6 +667,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       }
       lds_barrier();
       const int slot = sh.s_ovf;
+      ovf_full = slot < 0;
       if (slot >= 0) {  // else the record stays in staging (data loss is counted)
         uint8_t* dst = s.ovf_base + (int64_t)slot * kRawRecord;
 #pragma unroll
