@@ -82,8 +82,10 @@ struct AttnParams {
 // page) per unit (sequence -1: idle), [2 + 2 units, 2 + 4 units) (first
 // unit, chunks) per sequence -- the reference's layout --, then at
 // ud_offset(units) 8 ints per unit (sequence, first page, pages, context,
-// first unit, chunks, block of page 0, block of page 1), then units * kvh
-// merge counters.
+// first unit, chunks, block of page 0, block of page 1).  The units * kvh
+// merge counters are the last words of the plan buffer: their place does not
+// depend on ``units``, so counters left at zero by a call stay zero for the
+// next one even when its unit count (and so its plan layout) differs.
 __host__ __device__ __forceinline__ int ud_offset(int units) { return (2 + 4 * units + 7) & ~7; }
 
 __device__ __forceinline__ int pages_of(const int32_t* seq_lens, int b) { return (seq_lens[b] + 127) >> 7; }
@@ -127,8 +129,8 @@ struct Divider {  // x / d for 0 <= x < 2^24, 1 <= d
 
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __restrict__ seq_lens,
                                                             const int32_t* __restrict__ block_table, int64_t bt_stride,
-                                                            int32_t* __restrict__ plan, int batch, int units, int kvh,
-                                                            int slots) {
+                                                            int32_t* __restrict__ plan, int64_t plan_elems, int batch,
+                                                            int units, int kvh, int slots) {
   __shared__ int firsts[kPlanLds + 1];
   __shared__ unsigned long long best;
   __shared__ int shared_used;
@@ -228,9 +230,10 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __res
     ud[0] = make_int4(b, p0, np, seq);
     ud[1] = make_int4(first, c, bt[p0], np > 1 ? bt[p0 + 1] : 0);
   }
-  // merge counters of the fused merge; the last arrival of a (sequence,
-  // head) resets its counter, so zeroing is needed only here
-  for (int x = threadIdx.x; x < units * kvh; x += kPlanThreads) plan[ud0 + 8 * units + x] = 0;
+  // merge counters of the fused merge, for every unit count the buffer
+  // holds: everything past this plan's words.  The last arrival of a
+  // (sequence, head) resets its counter, so zeroing is needed only here.
+  for (int64_t x = ud0 + 8 * units + threadIdx.x; x < plan_elems; x += kPlanThreads) plan[x] = 0;
 }
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
@@ -918,7 +921,7 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.out = static_cast<uint16_t*>(out);
   p.out_stride = out_stride;
   p.ud_off = ud_offset((int)units);
-  p.done = plan + p.ud_off + 8 * units;
+  p.done = plan + plan_elems - units * kv_heads;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   const int slots = decode_slots();
   FP_CHECK(slots > 0, "cannot query the device's compute-unit count");
@@ -928,7 +931,7 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.inline_plan = replan == 2 && batch <= 64;
   if (replan && !p.inline_plan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
-                       (int)batch, (int)units, (int)kv_heads, slots);
+                       plan_elems, (int)batch, (int)units, (int)kv_heads, slots);
     FP_LAUNCH_CHECK();
   }
   // persistent grid: one resident wave of workgroups (slots over all KV

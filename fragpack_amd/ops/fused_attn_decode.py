@@ -84,7 +84,8 @@ def workspace_elems(kv_heads: int, units: int) -> tuple[int, int, int]:
 
     ``plan`` holds the reference's ``2 + 4 * units`` planner words (padded to
     8), an 8-int descriptor per unit and ``units * kv_heads`` counters for the
-    merge fused into the attention kernel.
+    merge fused into the attention kernel.  The counters are the buffer's last
+    words, so a workspace made for ``units`` serves calls with fewer units.
     """
     rows = kv_heads * units * GQA
     return rows * 128, rows * 2, ((2 + 4 * units + 7) & ~7) + 8 * units + units * kv_heads

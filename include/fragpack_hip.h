@@ -61,7 +61,10 @@ int fp_abi_version(void);
  *   plut        uint32 [2, H, 2], slut uint8 [2, H, 16]
  *   block_table int32 [B, bt_stride], seq_lens int32 [B]
  *   opart/ml/plan  workspace (float, float, int32) of at least
- *               H*units*8*128, H*units*16 and 2 + 4*units elements
+ *               H*units*8*128, H*units*16 and
+ *               ((2 + 4*units + 7) & ~7) + 8*units + H*units elements; the
+ *               plan buffer's last H*units words are the merge counters, so
+ *               one workspace serves calls of any unit count it fits (same H)
  *   out         BF16 [B, H * group, 128], out_stride elements between rows
  *   group       query heads per KV head: 1, 2, 4 or 8 (the reference pads
  *               smaller groups to 8 on the host; this kernel takes them as is)

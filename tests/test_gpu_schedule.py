@@ -288,3 +288,32 @@ def test_small_batch_plans_inside_the_attention_kernel(encoded_store, group):
         torch.cuda.synchronize()
         _check_outputs(queries, outputs, source, table, lengths)
         _check_plan(ws[2], lengths, units)
+
+
+def test_one_workspace_serves_steps_of_changing_batch(encoded_store):
+    """A serving engine sizes one workspace for its largest batch and then
+    decodes steps whose batch, and so unit count and plan layout, changes
+    from step to step (first layer replans, the others reuse).  The merge
+    counters sit at a place that does not move with the unit count, so every
+    step's outputs match fp32 attention, inline planning included."""
+    import torch
+
+    from fragpack_amd.ops.fused_attn_decode import decode_units
+
+    store, _arenas, source = encoded_store
+    sms = torch.cuda.get_device_properties(source.device).multi_processor_count
+    ws = _workspace(decode_units(96, HEADS, sms), source.device)  # batches above 64 use the planner launch
+    gen = torch.Generator(device=source.device).manual_seed(77)
+    rng = np.random.default_rng(77)
+    for batch in (3, 2, 5, 64, 1, 40, 2, 80, 3):
+        print("schedule batch", batch, flush=True)
+        units = decode_units(batch, HEADS, sms)
+        table = _block_table(batch)
+        lengths = rng.integers(1, 20 * TOKENS, batch).astype(np.int32)
+        queries = [torch.randn(batch, HEADS * 4, DIM, dtype=torch.bfloat16, device=source.device, generator=gen)
+                   for _ in range(LAYERS)]
+        outputs = [torch.full_like(q, float("nan")) for q in queries]
+        _decode_layers(store, queries, outputs, torch.from_numpy(table).to(source.device),
+                       torch.from_numpy(lengths).to(source.device), units, ws)
+        torch.cuda.synchronize()
+        _check_outputs(queries, outputs, source, table, lengths)
