@@ -28,6 +28,9 @@ def command(out: Path = OUT) -> list[str]:
         "-fPIC",
         "-shared",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # the kernels never produce or test for NaN; without this every
+        # fmaxf of an MFMA result is preceded by a canonicalising v_max
+        "-fno-honor-nans",
         "-Wno-unused-command-line-argument",
         f"-I{ROOT / 'include'}",
         "-o", str(out),

@@ -555,10 +555,8 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
     gm = nm;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.x * inv)) |
-                      ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.y * inv)) << 16);
-  const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.z * inv)) |
-                      ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc.w * inv)) << 16);
+  const uint32_t lo = pack_bf16x2(acc.x * inv, acc.y * inv);
+  const uint32_t hi = pack_bf16x2(acc.z * inv, acc.w * inv);
   *reinterpret_cast<uint2*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + g) * kDim + d) =
       make_uint2(lo, hi);
 }
@@ -758,10 +756,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
         if (hh == 0) {
           uint8_t* base = sh.pt + ((n * 4 + w) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1);
-          auto pk = [](float x, float y) {
-            return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) |
-                   ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
-          };
+          auto pk = pack_bf16x2;
           *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e0[1]);
           *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e0[3]);
           *reinterpret_cast<uint32_t*>(base + 4) = pk(e1[0], e1[1]);
@@ -820,10 +815,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       // the whole sequence in one unit: normalise and write the output rows
       if (hh == 0 && n < p.group) {
         const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
-        auto pk = [](float x, float y) {
-          return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) |
-                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
-        };
+        auto pk = pack_bf16x2;
         uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + n) * kDim + 32 * w +
                          16 * (c >> 1) + 4 * (c & 1);
         *reinterpret_cast<uint2*>(orow) = make_uint2(pk(o0[0] * inv, o0[1] * inv), pk(o0[2] * inv, o0[3] * inv));

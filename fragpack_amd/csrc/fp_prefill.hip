@@ -74,8 +74,12 @@ __device__ __forceinline__ pf_f32x4 pf_mfma(const uint4& a, const uint4& b, pf_f
                                                   c, 0, 0, 0);
 }
 
+// Two floats -> BF16 pair (x low), round to nearest even: one v_cvt_pk_bf16_f32.
+typedef float pf_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 pf_bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y) << 16);
+  const pf_f32x2 v = {x, y};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, pf_bf16x2));
 }
 
 __device__ __forceinline__ uint32_t pf_perm(uint32_t hi, uint32_t lo, uint32_t sel) {

@@ -60,6 +60,14 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Two floats -> BF16 pair (x low), round to nearest even: one v_cvt_pk_bf16_f32.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
+  const f32x2_t v = {x, y};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   // v_perm_b32: byte i of the result is byte sel.byte[i] of {hi:lo}
   // (0-3 from lo, 4-7 from hi, 12 -> 0x00).
@@ -314,7 +322,7 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
     // primary high bytes of scalars 0,2,4,6 / 1,3,5,7 (escape code 7 -> 0)
     const uint32_t hp_ev = perm(lut1, lut0, sk & 0x07070707u);
     const uint32_t hp_od = perm(lut1, lut0, (sk >> 4) & 0x07070707u);
-    // escape window: bytes eo .. eo+7 of the expanded escape stream
+    // escape window: the next 8 bytes of the expanded escape stream
     const int a = eo & ~3;
     const uint32_t* ew = reinterpret_cast<const uint32_t*>(esc + a);
     const uint32_t d0 = ew[0], d1 = ew[1], d2 = ew[2];
