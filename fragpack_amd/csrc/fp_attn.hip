@@ -690,24 +690,36 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     FP_STAMP(2);
     expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
     expand_var(vr, vv, w, lane, vlut.s, sh.esc[0][1], sh.hdr[0][1]);
+    // page 1's variable regions: each page's are in flight a page before
+    // they are expanded
+    RecRef nkr = kr, nvr = vr;
+    if (npages > 1) {
+      nkr = page_ref(meta, 1, 0);
+      nvr = page_ref(meta, 1, 1);
+    }
     __syncthreads();
     patch_raw(kr, vk, w, lane, sh.esc[0][0], sh.hdr[0][0]);
     patch_raw(vr, vv, w, lane, sh.esc[0][1], sh.hdr[0][1]);
+    if (npages > 1) {
+      vk = prefetch_var(nkr, w, lane);
+      vv = prefetch_var(nvr, w, lane);
+    }
 
     for (int i = 0; i < npages; ++i) {
       const int par = i & 1;
-      const bool more = i + 1 < npages;
+      const bool more = i + 1 < npages, more2 = i + 2 < npages;
       const int tok0 = (p0 + i) * kTokens;
-      if (more && ((i + 1) & 63) == 0) meta = load_meta(p, load_block(bt, i + 1, npages, lane), h);
-      // V slab of this page in flight while K is decoded; the next page's
-      // variable regions in flight for the whole page
+      if (more2 && ((i + 2) & 63) == 0) meta = load_meta(p, load_block(bt, i + 2, npages, lane), h);
+      // V slab of this page in flight while K is decoded; the variable
+      // regions of the page after next in flight for a whole page
       prefetch_dense(vr, w, nt, fv);
-      RecRef nkr = kr, nvr = vr;
-      if (more) {
-        nkr = page_ref(meta, i + 1, 0);
-        nvr = page_ref(meta, i + 1, 1);
-        vk = prefetch_var(nkr, w, lane);
-        vv = prefetch_var(nvr, w, lane);
+      RecRef nnkr = nkr, nnvr = nvr;
+      uint2 vk2 = make_uint2(0u, 0u), vv2 = make_uint2(0u, 0u);
+      if (more2) {
+        nnkr = page_ref(meta, i + 2, 0);
+        nnvr = page_ref(meta, i + 2, 1);
+        vk2 = prefetch_var(nnkr, w, lane);
+        vv2 = prefetch_var(nnvr, w, lane);
       }
       __syncthreads();  // B1: this page's escapes patched; the previous page's V pass done everywhere
       FP_STAMP(3 + 5 * min(i, 4));
@@ -800,6 +812,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                   });
       kr = nkr;
       vr = nvr;
+      nkr = nnkr;
+      nvr = nnvr;
+      vk = vk2;
+      vv = vv2;
       FP_STAMP(7 + 5 * min(i, 4));
     }
 
