@@ -339,6 +339,8 @@ def main() -> None:
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--no-large", action="store_true", help="skip the config-4 decode shape leg")
     ap.add_argument("--large-steps", type=int, default=20)
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the batch-64 context sweep (8K and 16K, both arms) beside config 4's 32K")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3x (scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -388,6 +390,28 @@ def main() -> None:
         torch.cuda.empty_cache()
         if not args.no_raw_arm:
             large_raw = decode_bench(torch, largs, raw=True)
+            for k in ("store", "arena"):
+                large_raw.pop(k)
+    sweep = []
+    if not args.no_sweep and not args.no_raw_arm:
+        # config 4's batch and heads at 8K and 16K context: where compressed
+        # records start to pay off against the BF16 paged arm
+        for ctx in (8192, 16384):
+            sargs = argparse.Namespace(**vars(args))
+            sargs.batch, sargs.heads, sargs.group, sargs.context = 64, 8, 4, ctx
+            sargs.steps, sargs.warmup, sargs.units = 50, 5, 0
+            torch.cuda.empty_cache()
+            arms = []
+            for raw_arm in (False, True):
+                r = decode_bench(torch, sargs, raw=raw_arm)
+                for k in ("store", "arena"):
+                    r.pop(k)
+                arms.append(r)
+            sweep.append({"context": ctx, "batch": 64, "kv_heads": 8, "group": 4,
+                          "compressed_us_per_step": round(arms[0]["step_ms"] * 1e3, 1),
+                          "bf16_paged_us_per_step": round(arms[1]["step_ms"] * 1e3, 1),
+                          "compressed_step_speedup": round(arms[1]["step_ms"] / arms[0]["step_ms"], 3),
+                          "validated": arms[0]["valid"] and arms[1]["valid"]})
     step_s = res["step_ms"] / 1e3
     kern_s = res["kern_ms"] / 1e3
     achieved = res["algo_bytes"] / kern_s / 1e9
@@ -452,6 +476,8 @@ def main() -> None:
                 "kernel_us": round(large_raw["kern_ms"] * 1e3, 1), "validated": large_raw["valid"],
                 "compressed_step_speedup": round(large_raw["step_ms"] / large["step_ms"], 3),
                 "hbm_GBps": round(large_raw["algo_bytes"] / (large_raw["kern_ms"] / 1e3) / 1e9, 1)}
+    if sweep:
+        line["context_sweep"] = sweep
     if enc is not None:
         line["encode"] = {"workload": f"config 3 shape: {args.encode_blocks} blocks x 8 KV heads x K/V, 10% "
                                       "Student-t(2)x16, overflow 8192",
