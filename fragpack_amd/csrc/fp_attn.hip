@@ -281,18 +281,18 @@ __device__ __forceinline__ uint4 a_frag(const uint4& w0, const uint4& w1, int j)
 // Lane of the natural (kernel-order) thread ``nt`` of a slab.
 __device__ __forceinline__ int lane_of_natural(int nt) { return 16 * (nt & 3) + 8 * (nt >> 5) + ((nt >> 2) & 7); }
 
-// A record as the workgroup sees it (uniform values).
+// A record as the workgroup sees it (uniform values): its address and length;
+// the 32 KB buffer resource over it is built at each use (two of its four
+// words are constants), which keeps three scalar registers per live record.
 struct RecRef {
-  rsrc_t rs;
+  uint32_t lo, hi;
   int vlen;  // bytes past the dense part; > kVarCap marks a raw record
+  __device__ __forceinline__ rsrc_t rs() const {
+    return make_rsrc(reinterpret_cast<const uint8_t*>((uint64_t)lo | ((uint64_t)hi << 32)), kRawRecord);
+  }
 };
 
-__device__ __forceinline__ RecRef make_ref(uint32_t lo, uint32_t hi, int vlen) {
-  RecRef r;
-  r.rs = make_rsrc(reinterpret_cast<const uint8_t*>((uint64_t)lo | ((uint64_t)hi << 32)), kRawRecord);
-  r.vlen = vlen;
-  return r;
-}
+__device__ __forceinline__ RecRef make_ref(uint32_t lo, uint32_t hi, int vlen) { return RecRef{lo, hi, vlen}; }
 
 // Record metadata of up to 64 pages of a unit, page i in lane i: K / V
 // record address (lo, hi) and length.
@@ -331,7 +331,7 @@ __device__ __forceinline__ RecRef page_ref(const PageMeta& m, int i, int kv) {
 
 // Dense words of the wave's slab ``slab`` of record ``r``.
 __device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt, SlabBuf& b) {
-  load_slab(r.rs, r.vlen > kVarCap, slab, nt, b);
+  load_slab(r.rs(), r.vlen > kVarCap, slab, nt, b);
 }
 
 // This lane's 8 bytes (at 512 w + 8 lane) of the record's variable region.
@@ -339,7 +339,7 @@ __device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt
 __device__ __forceinline__ bool quarter_used(const RecRef& r, int w) { return r.vlen <= kVarCap && 512 * w < r.vlen; }
 
 __device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane) {
-  return quarter_used(r, w) ? bld8(r.rs, 8 * lane, kDenseBytes + 512 * w) : make_uint2(0u, 0u);
+  return quarter_used(r, w) ? bld8(r.rs(), 8 * lane, kDenseBytes + 512 * w) : make_uint2(0u, 0u);
 }
 
 // Per-record escape staging, done by all four waves from their prefetched
@@ -399,14 +399,26 @@ __device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, in
 
 // Decodes this lane's kernel-order thread ``nt`` of the wave's slab ``w`` of
 // record ``r`` (escapes staged in ``esc``, header in ``hdr``) and calls
-// pair(a, word 2a, word 2a + 1, fragment a of ``tile``) for a = 0..3.
-template <typename Pair>
+// pair(a, word 2a, word 2a + 1, fragment a of ``tile``) for a = 0..3.  A raw
+// record's words come in natural slot order, a coded record's in even-odd
+// order (decode_words<true>): ``tile`` must be laid out in the same order,
+// or, with kTileEvenOdd, is always in even-odd order and is permuted here for
+// a raw record.
+template <bool kTileEvenOdd = false, typename Pair>
 __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, int w, int nt, NatPerm np,
                                             const HeadLut& lut, const uint8_t* esc, const uint32_t* hdr,
                                             const uint8_t* tile, int n, int c, Pair&& pair) {
   uint4 fr[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) fr[a] = tile_frag(tile, n, a, c);
+  if (kTileEvenOdd && r.vlen > kVarCap) {
+    // slots (4x + 2e + f) -> (4x + 2f + e): dwords (e0f0, e0f1), (e1f0, e1f1)
+    // become (f0e0, f0e1), (f1e0, f1e1)
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      fr[a] = make_uint4(perm(fr[a].y, fr[a].x, 0x05040100u), perm(fr[a].y, fr[a].x, 0x07060302u),
+                         perm(fr[a].w, fr[a].z, 0x05040100u), perm(fr[a].w, fr[a].z, 0x07060302u));
+  }
   uint4 prev;
   auto emit = [&](auto st_c, const uint4& wd) {
     constexpr int st = decltype(st_c)::value;
@@ -416,12 +428,12 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
       prev = wd;
   };
   if (r.vlen > kVarCap) {
-    raw_words(b, r.rs, w, nt, emit);
+    raw_words(b, r.rs(), w, nt, emit);
     return;
   }
   const int e0 = (int)(hdr[4 + w] & 0xFFFFu);  // esc_prefix[2 w]
   const int excl = natural_prefix(thread_escapes(b), np);
-  decode_words(b, esc, e0 + excl, lut.p0, lut.p1, emit);
+  decode_words<true>(b, esc, e0 + excl, lut.p0, lut.p1, emit);
 }
 
 // Optional per-workgroup timeline (built only with -DFP_TRACE): slot k of
@@ -444,7 +456,7 @@ struct AttnShared {
   uint8_t esc[2][2][kEscLds];  // [page parity][K, V] expanded escape bytes
   uint32_t hdr[2][2][12];      // [page parity][K, V] record headers
   uint8_t pt[kTileBytes];      // P tile
-  uint8_t qt[kTileBytes];      // Q tile
+  uint8_t qt[kTileBytes];      // Q tile, even-odd slot order
   float red[kWaves][8];        // per-wave page max / final l per head
   int last;
 };
@@ -669,9 +681,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
     __syncthreads();  // the previous unit is done with every tile
     FP_STAMP(1);
-    // Q into the fragment tile: u32 pair j of row r goes to fragment
-    // (r, a = j / 16, c = j % 4) at word x = (j % 16) / 4, i.e. the dims of
-    // slot i = 4x + 2f + e of (a, c) are 32a + 16x + 8f + 2c + e.
+    // Q into the fragment tile: u32 pair j of row r (dims 2j, 2j + 1 =
+    // 32a + 16x + 8f + 2c + e, e = 0, 1) belongs to fragment (r, a, c) at
+    // slot 4x + 2e + f (even-odd order; raw K records permute the fragments
+    // to natural order 4x + 2f + e in registers).
     if (w == 0) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
@@ -680,7 +693,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int j = 4 * (L & 15) + t;
-          *reinterpret_cast<uint32_t*>(sh.qt + ((row * 4 + (j >> 4)) * 4 + (j & 3)) * 16 + 4 * ((j >> 2) & 3)) = v[t];
+          const int frag = ((row * 4 + (j >> 4)) * 4 + (j & 3)) * 16, x = (j >> 3) & 1, f = (j >> 2) & 1;
+          // lanes L and L ^ 1 hold f = 0 and f = 1 of the same (a, c, x):
+          // each writes the dword of e = its own f
+          const uint32_t o = __shfl_xor(v[t], 1, 64);
+          *reinterpret_cast<uint32_t*>(sh.qt + frag + 8 * x + 4 * f) =
+              f ? perm(v[t], o, 0x07060302u) : perm(o, v[t], 0x05040100u);
         }
       }
     }
@@ -726,7 +744,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      decode_slab(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0], sh.qt, n, c,
+      decode_slab<true>(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0], sh.qt, n, c,
                   [&](auto a, const uint4& w0, const uint4& w1, const uint4& qa) {
                     s0 = mfma(a_frag(w0, w1, 0), qa, s0);
                     s1 = mfma(a_frag(w0, w1, 1), qa, s1);
@@ -765,14 +783,16 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
           e1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], p.scale_log2, nm));
           psum += e0[r] + e1[r];
         }
-        // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1][f = j][e = r & 1]
+        // P[n][token] -> tile[n][a = w][c' = 2 (c & 1) + r / 2][x = c >> 1]
+        // at slot 4x + 2e + f (f = j, e = r & 1): the even-odd order coded
+        // words decode in (a raw V record permutes the fragments)
         if (hh == 0) {
           uint8_t* base = sh.pt + ((n * 4 + w) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1);
           auto pk = pack_bf16x2;
-          *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e0[1]);
-          *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e0[3]);
-          *reinterpret_cast<uint32_t*>(base + 4) = pk(e1[0], e1[1]);
-          *reinterpret_cast<uint32_t*>(base + 20) = pk(e1[2], e1[3]);
+          *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e1[0]);
+          *reinterpret_cast<uint32_t*>(base + 4) = pk(e0[1], e1[1]);
+          *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e1[2]);
+          *reinterpret_cast<uint32_t*>(base + 20) = pk(e0[3], e1[3]);
         }
       };
       if (spec) softmax_tile(m_run);
@@ -805,7 +825,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       FP_STAMP(6 + 5 * min(i, 4));
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
-      decode_slab(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
+      decode_slab<true>(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
                   [&](auto a, const uint4& w0, const uint4& w1, const uint4& pa) {
                     o0 = mfma(a_frag(w0, w1, 0), pa, o0);
                     o1 = mfma(a_frag(w0, w1, 1), pa, o1);

@@ -310,8 +310,10 @@ __device__ __forceinline__ void stage_escapes(Rd4&& rd4, const SlabHdr& h, const
 // calls emit(st, word) for st = 0..7, word = 4 dwords = 8 BF16 (little-endian
 // pairs).  ``eo`` is the LDS byte index (relative to ``esc``) of this
 // thread's first escape.  ``lut0``, ``lut1``: primary table bytes 0-3 / 4-6
-// (byte 7 = 0).
-template <typename Emit>
+// (byte 7 = 0).  Scalar order within a word: natural (dwords hold scalars
+// 0,1 | 2,3 | 4,5 | 6,7) or, with kEvenOdd, (0,2 | 1,3 | 4,6 | 5,7), which
+// takes two byte permutes fewer (the attention kernel's tiles follow it).
+template <bool kEvenOdd = false, typename Emit>
 __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* esc, int eo, uint32_t lut0,
                                              uint32_t lut1, Emit&& emit) {
   static_for<0, 8>([&](auto st_c) {
@@ -335,12 +337,17 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
     const uint32_t sel = (rank & m15) | (~m15 & 0xCCCCCCCCu);
     const uint32_t h_ev = hp_ev | perm(ehi, elo, sel & 0x0F0F0F0Fu);
     const uint32_t h_od = hp_od | perm(ehi, elo, (sel >> 4) & 0x0F0F0F0Fu);
-    const uint32_t h01 = perm(h_od, h_ev, 0x05010400u);  // high bytes of scalars 0..3
-    const uint32_t h23 = perm(h_od, h_ev, 0x07030602u);  // 4..7
     const uint4 lw = b.v[st >> 1];
-    const uint32_t la = (st & 1) ? lw.z : lw.x, lb = (st & 1) ? lw.w : lw.y;
-    emit(st_c, make_uint4(perm(h01, la, 0x05010400u), perm(h01, la, 0x07030602u), perm(h23, lb, 0x05010400u),
-                          perm(h23, lb, 0x07030602u)));
+    const uint32_t la = (st & 1) ? lw.z : lw.x, lb = (st & 1) ? lw.w : lw.y;  // low bytes of 0..3 / 4..7
+    if constexpr (kEvenOdd) {
+      emit(st_c, make_uint4(perm(h_ev, la, 0x05020400u), perm(h_od, la, 0x05030401u), perm(h_ev, lb, 0x07020600u),
+                            perm(h_od, lb, 0x07030601u)));
+    } else {
+      const uint32_t h01 = perm(h_od, h_ev, 0x05010400u);  // high bytes of scalars 0..3
+      const uint32_t h23 = perm(h_od, h_ev, 0x07030602u);  // 4..7
+      emit(st_c, make_uint4(perm(h01, la, 0x05010400u), perm(h01, la, 0x07030602u), perm(h23, lb, 0x05010400u),
+                            perm(h23, lb, 0x07030602u)));
+    }
   });
 }
 
