@@ -267,6 +267,106 @@ def encode_bench(torch, args) -> dict:
                 spills=int(c[8]), err_overflow=int(c[5]))
 
 
+def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int, close: bool,
+                     rounds: int = 20) -> dict:
+    """One decode step of one layer as a serving engine runs it (reference:
+    benchmarks/fragpack_step_bench.py:472-610): write the step's B new
+    tokens into staging, attend over the compressed records (the open last
+    block read from staging), encode the blocks the step closes.  Each
+    sequence has ``pages`` blocks; its last block holds 127 tokens before
+    the step (``close``: the step's token fills it, all B blocks are encoded)
+    or 100 (nothing closes).  Every sample re-seeds the open blocks outside
+    the timed region (prepare / write / commit), as the reference does; the
+    timed region is write -> decode attention -> encode with HIP events
+    between them, enqueued behind a spinning kernel so that the events see
+    the GPU's time (kernels and launch gaps) rather than the host's.  Validated: the encode counter moves by 2 H B (close) or 0,
+    and the last blocks gather back bit-exact."""
+    import statistics
+
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+
+    B, H, G = batch, heads, group
+    offset = 127 if close else 100
+    nb = B * pages
+    rng = np.random.default_rng(args.seed + 7)
+    scales = channel_scales(rng, H, 0.02)
+    tables = device_tables(calibrated_tables(rng, H, scales), "cuda")
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 7)
+    scales_t = torch.from_numpy(scales).float().cuda()
+    arena = torch.empty((nb, page_bytes(H)), dtype=torch.uint8, device="cuda")
+    fill = 64
+    store = HbmKvStore([arena], H, tables, max_tokens=max(fill, B) * T, staging_slots=B, overflow_records=256)
+    no_live = np.zeros(0, np.int32)
+    full = [b * pages + p for b in range(B) for p in range(pages - 1)]
+    for i in range(0, len(full), fill):
+        blocks = torch.tensor(full[i : i + fill], dtype=torch.int64, device="cuda")
+        slots = (blocks[:, None] * T + torch.arange(T, device="cuda")).reshape(-1)
+        kv = gen_kv(torch, gen, slots.numel(), H, scales_t)
+        store.prepare(slots, slots.numel(), no_live)
+        store.write(0, kv[0], kv[1], slots)
+        store.encode(0, blocks.numel())
+        store.commit()
+    last = torch.arange(B, device="cuda", dtype=torch.int64) * pages + pages - 1
+    live = last.to(torch.int32).cpu().numpy()
+    seed_slots = (last[:, None] * T + torch.arange(offset, device="cuda")).reshape(-1)
+    seed = gen_kv(torch, gen, seed_slots.numel(), H, scales_t)
+    step_slots = last * T + offset
+    step_kv = gen_kv(torch, gen, B, H, scales_t)
+    bt = (torch.arange(B, device="cuda")[:, None] * pages + torch.arange(pages, device="cuda")).to(torch.int32)
+    lens = torch.full((B,), (pages - 1) * T + offset + 1, dtype=torch.int32, device="cuda")
+    q = torch.randn((B, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    units = decode_units(B, H, sms)
+    o_e, m_e, p_e = workspace_elems(H, units)
+    ws = (torch.empty(o_e, device="cuda"), torch.empty(m_e, device="cuda"),
+          torch.empty(p_e, dtype=torch.int32, device="cuda"))
+    tabs = RecordTables(*store.layer_tables(0))
+    wk = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
+    wv = torch.empty_like(wk)
+    want_k = torch.cat((seed[0].view(B, offset, H, D), step_kv[0].view(B, 1, H, D)), dim=1)
+    want_v = torch.cat((seed[1].view(B, offset, H, D), step_kv[1].view(B, 1, H, D)), dim=1)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    samples = {"write": [], "attention": [], "encode": [], "layer": []}
+    valid = True
+    for it in range(rounds + 3):
+        store.prepare(seed_slots, seed_slots.numel(), no_live)
+        store.write(0, seed[0], seed[1], seed_slots)
+        store.commit()
+        store.prepare(step_slots, B, live)
+        before = int(store.counters[7].item())
+        # the GPU spins while the three operations are enqueued, so the
+        # events time the GPU's work and launch gaps, not the host's enqueue
+        torch.cuda._sleep(2_000_000)
+        ev[0].record()
+        store.write(0, step_kv[0], step_kv[1], step_slots)
+        ev[1].record()
+        decode_attention(q, tabs, bt, lens, D ** -0.5, units, out, ws, True)
+        ev[2].record()
+        store.encode(0, B)
+        ev[3].record()
+        ev[3].synchronize()
+        store.commit()
+        encoded = int(store.counters[7].item()) - before
+        store.gather(0, last.to(torch.int32), wk, wv)
+        ok = (encoded == (2 * H * B if close else 0)
+              and torch.equal(wk[:, : offset + 1].view(torch.int16), want_k.view(torch.int16))
+              and torch.equal(wv[:, : offset + 1].view(torch.int16), want_v.view(torch.int16))
+              and bool(torch.isfinite(out.float()).all()))
+        valid = valid and ok
+        if it >= 3:
+            for k, (a, b) in (("write", (0, 1)), ("attention", (1, 2)), ("encode", (2, 3)), ("layer", (0, 3))):
+                samples[k].append(ev[a].elapsed_time(ev[b]) * 1e3)
+    res = {f"us_{k}": round(statistics.median(v), 1) for k, v in samples.items()}
+    res.update({"batch": B, "kv_heads": H, "group": G, "context_after_step": int(lens[0].item()),
+                "case": "close_block" if close else "mid_block", "validated": valid})
+    log(f"layer step B{B} H{H} {res['case']}: write {res['us_write']} us, attention {res['us_attention']} us, "
+        f"encode {res['us_encode']} us, layer {res['us_layer']} us, valid {valid}")
+    return res
+
+
 def cpu_baseline(torch, res, args) -> dict:
     """The CPU oracle (C, OpenMP) on the same decode step: decode every record
     of the 4 x 8192-token layer and run fp32 attention, timed on this host's
@@ -339,6 +439,8 @@ def main() -> None:
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--no-large", action="store_true", help="skip the config-4 decode shape leg")
     ap.add_argument("--large-steps", type=int, default=20)
+    ap.add_argument("--no-layer-step", action="store_true",
+                    help="skip the per-layer serving step legs (write, attention, encode)")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the batch-64 context sweep (8K and 16K, both arms) beside config 4's 32K")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -392,6 +494,14 @@ def main() -> None:
             large_raw = decode_bench(torch, largs, raw=True)
             for k in ("store", "arena"):
                 large_raw.pop(k)
+    layer_steps = []
+    if not args.no_layer_step:
+        # one layer of a serving decode step: config 1's shape and config 4's
+        # batch / heads at 8K, with and without closing blocks
+        for shape in ((args.batch, args.heads, args.group, math.ceil(args.context / T)), (64, 8, 4, 64)):
+            for close in (False, True):
+                torch.cuda.empty_cache()
+                layer_steps.append(layer_step_bench(torch, args, *shape, close=close))
     sweep = []
     if not args.no_sweep and not args.no_raw_arm:
         # config 4's batch and heads at 8K and 16K context: where compressed
@@ -478,6 +588,8 @@ def main() -> None:
                 "hbm_GBps": round(large_raw["algo_bytes"] / (large_raw["kern_ms"] / 1e3) / 1e9, 1)}
     if sweep:
         line["context_sweep"] = sweep
+    if layer_steps:
+        line["layer_step"] = layer_steps
     if enc is not None:
         line["encode"] = {"workload": f"config 3 shape: {args.encode_blocks} blocks x 8 KV heads x K/V, 10% "
                                       "Student-t(2)x16, overflow 8192",

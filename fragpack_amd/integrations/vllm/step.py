@@ -111,7 +111,7 @@ def plan_step(
     slot_rows: int,
     workspace_pages: int,
     max_tokens: int,
-    with_prefills: bool = True,
+    capture: bool = False,
 ) -> HostStep:
     """Plan one step from the batch's host metadata (backend.py:269-290).
 
@@ -121,7 +121,8 @@ def plan_step(
         slot_rows: Rows of the slot mapping (bounds ``num_tokens``).
         workspace_pages: Pages of the BF16 prefill workspace.
         max_tokens: Largest step the store was sized for.
-        with_prefills: False for a graph-capture build (no groups).
+        capture: A graph-capture build: no prefill groups, and an encode
+            grid that covers every replay of the captured decode shape.
 
     Raises:
         ValueError: A prefill row needs more pages than the workspace holds.
@@ -134,11 +135,14 @@ def plan_step(
     num_tokens = min(int(qsl[num_reqs]), slot_rows)
     # one close per 128-token boundary crossed by the row's new tokens
     closes = int(np.sum(seq // BLOCK_TOKENS - np.maximum(seq - qlen, 0) // BLOCK_TOKENS))
-    # decode-only batches keep the grid of their captured shape: each decode
-    # closes at most one block
-    max_close = min(max(closes, nd), max_tokens)
+    # A captured decode shape encodes with a grid that covers every replay
+    # (each decode closes at most one block).  Any other build is launched
+    # as planned, so its grid is the exact close count and a step that
+    # closes nothing launches no encode (the reference always sizes the grid
+    # for capture, backend.py:287).
+    max_close = min(max(closes, nd) if capture else closes, max_tokens)
     prefills: list[HostPrefillGroup] = []
-    if with_prefills and nd < num_reqs:
+    if not capture and nd < num_reqs:
         prefills = prefill_groups(qsl, seq, nd, workspace_pages)
     return HostStep(num_reqs, nd, num_tokens, closes, max_close, prefills)
 
@@ -355,7 +359,7 @@ class FragPackRunner:
 
         store = self.bind(caches)
         hs = plan_step(query_start_loc, seq_lens_host, slot_mapping.shape[0], self.workspace_pages,
-                       self.max_tokens, with_prefills=not capture)
+                       self.max_tokens, capture=capture)
         if not capture:
             store.prepare(slot_mapping, hs.num_tokens, live_blocks)
             self.steps += 1

@@ -248,8 +248,11 @@ def test_closes_count_blocks_filled_this_step_brute_force():
         # a block closes when its 128th token (position 128k-1) is among the new ones
         brute = sum(1 for r in range(R) for pos in range(prior[r], seq[r]) if pos % 128 == 127)
         assert hs.closes == brute
-        assert hs.max_close == min(max(brute, hs.num_decodes), 4096)
+        assert hs.max_close == min(brute, 4096)  # launched as planned: the exact count
         assert hs.num_tokens == qsl[-1]
+        cap = plan_step(qsl, seq, slot_rows=int(qsl[-1]) + 3, workspace_pages=64, max_tokens=4096, capture=True)
+        assert cap.max_close == min(max(brute, cap.num_decodes), 4096)  # covers every replay
+        assert cap.prefills == []
 
 
 def test_prefill_groups_pack_rows_in_order_within_the_workspace():
@@ -289,8 +292,7 @@ def test_prefill_longer_than_the_workspace_is_rejected():
 
     with pytest.raises(ValueError, match="workspace"):
         plan_step(np.array([0, 600]), np.array([3000]), 600, workspace_pages=8, max_tokens=4096)
-    hs = plan_step(np.array([0, 600]), np.array([3000]), 600, workspace_pages=8, max_tokens=4096,
-                   with_prefills=False)
+    hs = plan_step(np.array([0, 600]), np.array([3000]), 600, workspace_pages=8, max_tokens=4096, capture=True)
     assert hs.prefills == [] and hs.num_decodes == 0
 
 
