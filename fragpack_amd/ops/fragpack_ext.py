@@ -107,6 +107,9 @@ class Extension:
         sigs = {
             "fp_fused_decode": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p,
                                 _i64, _p, _i64, _i64, _i32, _f64, _p],
+            "fp_fused_decode_append": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64,
+                                       _p, _i64, _p, _i64, _i64, _i32, _f64, _p, _i64, _i64, _p, _i64, _i64, _p,
+                                       _p, _i64, _p, _i64, _p],
             "fp_hbm_prepare": [sp, _p, _i64, _p, _i64, _i64, _p],
             "fp_hbm_write": [sp, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p],
             "fp_hbm_encode": [sp, _p, _i64, _i64, _i64, _i64, _i64, _p],
@@ -124,6 +127,7 @@ class Extension:
             fn.argtypes = args
             fn.restype = _i32
         self._fused = lib.fp_fused_decode
+        self._fused_append = lib.fp_fused_decode_append
         lib.fp_last_error.restype = ctypes.c_char_p
         lib.fp_abi_version.restype = _i32
 
@@ -133,7 +137,13 @@ class Extension:
 
     # -- fused_decode (fragpack_ext.cpp:5-9, fused_attn_decode.cu:429-478) --
     def fused_decode(self, q, rec_addr, rec_len, plut, slut, block_table, seq_lens, opart, ml, plan, out,
-                     units: int, replan: bool, scale: float, group: int = 8) -> None:
+                     units: int, replan: bool, scale: float, group: int = 8, append=None) -> None:
+        """``append``: None, or ``(new_k, new_v, slot_mapping, staging,
+        scratch)`` -- each sequence's new token (BF16 ``[B, H, 128]``, int64
+        slot, negative = padding) is written into its open block's raw record
+        inside the attention launch (the store's ``write`` for a decode-only
+        step); records outside the ``staging`` / ``scratch`` tensors are left
+        alone."""
         # one tuple read per tensor property: this runs once per decode layer
         qsh, qst, ost, bst = q.shape, q.stride(), out.stride(), block_table.stride()
         bf16, i32 = torch.bfloat16, torch.int32
@@ -157,14 +167,30 @@ class Extension:
         mode = 0
         if replan:
             mode = 2 if getattr(plan, "_fp_counters_zeroed", False) else 1
-        if self._fused(
+        args = (
             _dev(q, "q"), qst[0], B, kvh, group, _dev(rec_addr, "rec_addr"), _dev(rec_len, "rec_len"),
             _dev(plut, "plut"), _dev(slut, "slut"), _dev(block_table, "block_table"), bst[0],
             _dev(seq_lens, "seq_lens"), _dev(opart, "opart"), opart.numel(), _dev(ml, "ml"), ml.numel(),
             _dev(plan, "plan"), plan.numel(), _dev(out, "out"), ost[0], units, mode, scale,
-            torch.cuda.current_stream().cuda_stream,
-        ):
-            raise RuntimeError(f"fp_fused_decode: {self._lib.fp_last_error().decode()}")
+        )
+        if append is None:
+            if self._fused(*args, torch.cuda.current_stream().cuda_stream):
+                raise RuntimeError(f"fp_fused_decode: {self._lib.fp_last_error().decode()}")
+        else:
+            raise NotImplementedError("the fused append (fp_fused_decode_append) is disabled: its first GPU run "
+                                      "faulted and the cause is not yet found; write with HbmKvStore.write")
+            nk, nv, slots, staging, scratch = append
+            _check(slots.dtype == torch.int64 and slots.numel() >= B and slots.is_contiguous(),
+                   "slot_mapping must be int64 [>= B]")
+            for t, name in ((nk, "new_k"), (nv, "new_v")):
+                _check(t.dtype == bf16 and t.dim() == 3 and t.shape[0] >= B and t.shape[1] == kvh and t.shape[2] == 128
+                       and t.stride(2) == 1, f"{name} must be BF16 [B, H, 128] with contiguous rows")
+            if self._fused_append(
+                *args, _dev(nk, "new_k"), nk.stride(0), nk.stride(1), _dev(nv, "new_v"), nv.stride(0), nv.stride(1),
+                _dev(slots, "slot_mapping"), _dev(staging, "staging"), staging.numel() * staging.element_size(), _dev(scratch, "scratch"),
+                scratch.numel() * scratch.element_size(), torch.cuda.current_stream().cuda_stream,
+            ):
+                raise RuntimeError(f"fp_fused_decode_append: {self._lib.fp_last_error().decode()}")
         if mode:
             plan._fp_counters_zeroed = True
 

@@ -101,6 +101,7 @@ def decode_attention(
     out: torch.Tensor,
     workspace: tuple[torch.Tensor, torch.Tensor, torch.Tensor],
     replan: bool,
+    append: tuple | None = None,
 ) -> None:
     """Split-KV decode attention for one query token per sequence.
 
@@ -116,6 +117,14 @@ def decode_attention(
         workspace: ``(opart, ml, plan)`` sized by :func:`workspace_elems`.
         replan: Recompute the work plan from ``seq_lens`` and ``units``; later
             layers of the same step may pass False.
+        append: None, or ``(new_k, new_v, slot_mapping, staging, scratch)``:
+            write each sequence's new token (BF16 ``[B, H, 128]``, int64
+            slot, negative = padding; the sequence's last position) into its
+            open block's raw record first, in the same launch -- a
+            decode-only step's ``HbmKvStore.write`` fused into attention
+            (this build's addition; the reference writes with a launch of its
+            own).  ``staging`` / ``scratch`` are the store's tensors; records
+            outside them are never written.
 
     Raises:
         ValueError: If the query group does not divide ``GQA``.
@@ -128,10 +137,10 @@ def decode_attention(
     group = q.shape[1] // kv_heads
     if group * kv_heads != q.shape[1] or GQA % group:
         raise ValueError(f"query heads {q.shape[1]} need a group dividing {GQA}")
-    _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, replan, group)
+    _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, replan, group, append)
 
 
-def _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, replan, group=GQA) -> None:
+def _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, replan, group=GQA, append=None) -> None:
     extension().fused_decode(
         q,
         tables.rec_addr,
@@ -148,6 +157,7 @@ def _launch(q, tables, block_table, seq_lens, scale, units, out, workspace, repl
         replan,
         scale,
         group,
+        append,
     )
 
 

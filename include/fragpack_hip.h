@@ -80,6 +80,32 @@ int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_h
                     int64_t ml_elems, int32_t* plan, int64_t plan_elems, void* out, int64_t out_stride,
                     int64_t units, int replan, double scale, fp_stream_t stream);
 
+/*
+ * fp_fused_decode plus the store's write of a decode-only step, in one
+ * launch.  No counterpart in the reference, which writes with hbm_write
+ * (fragpack_ext.cpp:19-23, hbm_kv.cu:221-255) before fused_decode: here the
+ * unit that owns each sequence's last page first writes that sequence's new
+ * token -- new_k / new_v row b -- into slot slot_mapping[b] (block * 128 +
+ * row, negative: padding, nothing written) of the raw record the block's
+ * table entry names, then attends.  Only records that lie inside
+ * [staging, staging + staging_bytes) or [scratch, scratch + scratch_bytes)
+ * are written (a table entry elsewhere is skipped, as hbm_write skips a block
+ * without a staging slot).  Every row must be a decode row: one new token,
+ * the sequence's last (seq_lens[b] - 1), in its last block.
+ *   new_k, new_v  BF16 [B, H, 128]: token / head strides in elements (even)
+ *   slot_mapping  int64 [B]
+ */
+int fp_fused_decode_append(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
+                           const int64_t* rec_addr, const int32_t* rec_len, const uint32_t* plut,
+                           const uint8_t* slut, const int32_t* block_table, int64_t bt_stride,
+                           const int32_t* seq_lens, float* opart, int64_t opart_elems, float* ml,
+                           int64_t ml_elems, int32_t* plan, int64_t plan_elems, void* out, int64_t out_stride,
+                           int64_t units, int replan, double scale, const void* new_k, int64_t nk_token_stride,
+                           int64_t nk_head_stride, const void* new_v, int64_t nv_token_stride,
+                           int64_t nv_head_stride, const int64_t* slot_mapping, const void* staging,
+                           int64_t staging_bytes, const void* scratch, int64_t scratch_bytes,
+                           fp_stream_t stream);
+
 /* Step start: GC, staging claims, close list.  Replaces hbm_prepare
  * (fragpack_ext.cpp:11-17, hbm_kv.cu:669-686). */
 int fp_hbm_prepare(const fp_store_t* s, const int64_t* slot_mapping, int64_t n_tok, const int32_t* live,
