@@ -202,11 +202,12 @@ def prefill_bench(torch, args) -> dict:
     return dict(ms=ms, flops=flops, valid=valid, max_err=err.max().item())
 
 
-def encode_bench(torch, args) -> dict:
+def encode_bench(torch, args, ordered: bool = False) -> dict:
     """Store encode kernel over BASELINE config 3's shape: ``--encode-blocks``
     completed blocks x 8 KV heads x K/V, 10% Student-t(2) x 16 values, an
     8192-record overflow pool.  Times only the encode launches (fill and
-    overflow bitmap are reset between repetitions)."""
+    overflow bitmap are reset between repetitions).  ``ordered``: the
+    block-major encode that places each block's records in (kv, head) order."""
     H = 8
     n = args.encode_blocks
     rng = np.random.default_rng(args.seed + 3)
@@ -244,7 +245,7 @@ def encode_bench(torch, args) -> dict:
         store.rec_len.copy_(len0)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        store.encode(0, n)
+        store.encode(0, n, ordered=ordered)
         e1.record()
         torch.cuda.synchronize()
         if r:  # first launch is warmup
@@ -261,14 +262,14 @@ def encode_bench(torch, args) -> dict:
     written = int((DENSE + rec_len[coded]).sum()) + 32768 * int((in_ovf & ~coded).sum())
     records = n * 2 * H
     eff = records * 32768
-    log(f"encode: {records} records in {ms * 1e3:.0f} us -> {eff / ms / 1e6:.0f} GB/s effective, "
+    log(f"encode{' (ordered)' if ordered else ''}: {records} records in {ms * 1e3:.0f} us -> {eff / ms / 1e6:.0f} GB/s effective, "
         f"fallbacks {int(c[6])} (spills {int(c[8])}), overflow-full drops {int(c[5])}")
     return dict(ms=ms, records=records, eff_bytes=eff, read_write_bytes=eff + written, fallbacks=int(c[6]),
                 spills=int(c[8]), err_overflow=int(c[5]))
 
 
 def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int, close: bool,
-                     rounds: int = 20) -> dict:
+                     rounds: int = 20, ordered: bool = False) -> dict:
     """One decode step of one layer as a serving engine runs it (reference:
     benchmarks/fragpack_step_bench.py:472-610): write the step's B new
     tokens into staging, attend over the compressed records (the open last
@@ -345,7 +346,7 @@ def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int
         ev[1].record()
         decode_attention(q, tabs, bt, lens, D ** -0.5, units, out, ws, True)
         ev[2].record()
-        store.encode(0, B)
+        store.encode(0, B, ordered=ordered)
         ev[3].record()
         ev[3].synchronize()
         store.commit()
@@ -361,7 +362,8 @@ def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int
                 samples[k].append(ev[a].elapsed_time(ev[b]) * 1e3)
     res = {f"us_{k}": round(statistics.median(v), 1) for k, v in samples.items()}
     res.update({"batch": B, "kv_heads": H, "group": G, "context_after_step": int(lens[0].item()),
-                "case": "close_block" if close else "mid_block", "validated": valid})
+                "case": ("close_block" if close else "mid_block") + (" (ordered encode)" if ordered else ""),
+                "validated": valid})
     log(f"layer step B{B} H{H} {res['case']}: write {res['us_write']} us, attention {res['us_attention']} us, "
         f"encode {res['us_encode']} us, layer {res['us_layer']} us, valid {valid}")
     return res
@@ -467,6 +469,7 @@ def main() -> None:
     torch.cuda.set_device(int(os.environ.get("LOCAL_RANK", "0")))
     res = decode_bench(torch, args)
     enc = None if args.no_encode else encode_bench(torch, args)
+    enc_ordered = None if args.no_encode else encode_bench(torch, args, ordered=True)
     pre = None if args.no_prefill else prefill_bench(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(torch, res, args)
     raw = None
@@ -499,9 +502,9 @@ def main() -> None:
         # one layer of a serving decode step: config 1's shape and config 4's
         # batch / heads at 8K, with and without closing blocks
         for shape in ((args.batch, args.heads, args.group, math.ceil(args.context / T)), (64, 8, 4, 64)):
-            for close in (False, True):
+            for close, ordered in ((False, False), (True, False), (True, True)):
                 torch.cuda.empty_cache()
-                layer_steps.append(layer_step_bench(torch, args, *shape, close=close))
+                layer_steps.append(layer_step_bench(torch, args, *shape, close=close, ordered=ordered))
     sweep = []
     if not args.no_sweep and not args.no_raw_arm:
         # config 4's batch and heads at 8K and 16K context: where compressed
@@ -598,6 +601,12 @@ def main() -> None:
                           "hbm_GBps": round(enc["read_write_bytes"] / enc["ms"] / 1e6, 1),
                           "fallbacks": enc["fallbacks"], "spills": enc["spills"],
                           "overflow_full_drops": enc["err_overflow"]}
+        if enc_ordered is not None:
+            line["encode"]["ordered"] = {"what": "block-major encode placing each block's records in (kv, head) "
+                                                 "order: the same spill set on every run",
+                                         "us": round(enc_ordered["ms"] * 1e3, 1),
+                                         "effective_GBps": round(enc_ordered["eff_bytes"] / enc_ordered["ms"] / 1e6, 1),
+                                         "fallbacks": enc_ordered["fallbacks"], "spills": enc_ordered["spills"]}
     print(json.dumps(line))
 
 

@@ -527,6 +527,16 @@ __device__ uint64_t fp_enc_trace[1024 * 16];
   } while (0)
 #endif
 
+// kBlockMajor (the ordered encode): workgroup g encodes whole blocks
+// close_list[g], close_list[g + grid], ..., each block's 2H records in
+// (kv, head) order, and places them itself: a record that codes takes the
+// block's next kDenseBytes + var_len bytes if they fit in the page, else it
+// spills to the overflow pool; later records of the block still try.  The
+// placement then depends only on the records' sizes -- the same spill set on
+// every run (the reference's encode claims page space in arrival order, so
+// which record spills can change from run to run; its import places by a
+// prefix over the lengths, hbm_kv.cu:628-642).
+template <bool kBlockMajor>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kEncodeWgPerCu)))
 encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint8_t* rank_of) {
   __shared__ EncShared sh;
@@ -535,7 +545,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   const int per = 2 * s.H;
   const int n_closes = s.counters[kCloses];
   const int n_rec = n_closes * per;
-  int r = blockIdx.x;
+  int r = kBlockMajor ? (int)blockIdx.x * per : (int)blockIdx.x;
   if (r >= n_rec) return;
   // Record metadata (block, heir, staging slot) of this workgroup's records
   // in batches of 64 (record r + j grid in lane j), loaded with vector loads
@@ -543,13 +553,17 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   // The stage streams record r + grid while r is encoded.
   const int g = (int)gridDim.x;
   const int lane = tid & 63;
+  // the k-th record of this workgroup: its block (close index) and (kv, head)
+  auto rec_kvh = [&](int rr) { return kBlockMajor ? rr % per : rr / n_closes; };
+  auto next_rec = [&](int rr) { return kBlockMajor ? (rr % per == per - 1 ? rr + 1 + (g - 1) * per : rr + 1) : rr + g; };
   auto load_meta = [&](int k0, int& mb, int& mh, int& mw) {
     mb = 0;
     mh = -1;
     mw = 0;
-    const int rr = (int)blockIdx.x + (k0 + lane) * g;
-    if (rr < n_rec) {
-      const int ci = rr % n_closes;
+    const int kk = k0 + lane;
+    const int ci = kBlockMajor ? (int)blockIdx.x + (kk / per) * g : ((int)blockIdx.x + kk * g) % n_closes;
+    const bool ok = kBlockMajor ? ci < n_closes : (int)blockIdx.x + kk * g < n_rec;
+    if (ok) {
       mb = s.close_list[ci];
       mh = s.close_list[s.cap + ci];
       mw = s.wslot[mb];
@@ -560,18 +574,19 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   load_meta(64, nb, nh, nw);
   int b = __builtin_amdgcn_readfirstlane(cb);
   int heir = __builtin_amdgcn_readfirstlane(ch);
-  uint8_t* src = staging_addr(s, __builtin_amdgcn_readfirstlane(cw), layer, r / n_closes);
+  uint8_t* src = staging_addr(s, __builtin_amdgcn_readfirstlane(cw), layer, rec_kvh(r));
   stage_record(stage, src);
   int rank_kvh = -1;
   // counter increments of this workgroup (thread 0), added once at the end:
   // one hot counter hit by every record serialises at its memory channel
   int n_enc = 0, n_fall = 0, n_err = 0, n_spill = 0;
   bool ovf_full = false;  // this workgroup found the overflow pool full
+  int boff = 0;           // ordered encode: the block's next free page byte (thread 0)
 #ifdef FP_TRACE_ENC
   uint64_t enc_tacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #endif
-  for (int k = 0; r < n_rec; r += g, ++k) {
-    const int kvh = r / n_closes;
+  for (int k = 0; r < n_rec; r = next_rec(r), ++k) {
+    const int kvh = rec_kvh(r);
     ENC_STAMP(0);
     const int64_t idx = ((int64_t)layer * s.NB + b) * per + kvh;
     int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
@@ -582,7 +597,11 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
     // the fill value is only a first guess for the claim: fetch it early
     int cur = 0;
-    if (tid == 0) cur = __hip_atomic_load(fill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kBlockMajor) {
+      if (tid == 0 && kvh == 0) boff = *fill;  // only this workgroup places this block's records
+    } else if (tid == 0) {
+      cur = __hip_atomic_load(fill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // this record's words: the wave's own LDS loads, then into registers
     __builtin_amdgcn_s_waitcnt(0);
     uint4 wd[8];
@@ -597,8 +616,9 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     const int heir1 = __builtin_amdgcn_readlane(nbatch ? nh : ch, k1);
     const int w1 = __builtin_amdgcn_readlane(nbatch ? nw : cw, k1);
     uint8_t* src1 = src;
-    if (r + g < n_rec) {
-      src1 = staging_addr(s, w1, layer, (r + g) / n_closes);
+    const int r1 = next_rec(r);
+    if (r1 < n_rec) {
+      src1 = staging_addr(s, w1, layer, rec_kvh(r1));
       stage_record(stage, src1);
     }
     if (nbatch) {  // the next batch becomes current; load the one after
@@ -620,7 +640,17 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     int eo, ro;
     const EncResult res = enc_analyse(wd, sh, sym, code, nib, eo, ro);
     ENC_STAMP(3);
-    if (res.codes) {
+    if (kBlockMajor && res.codes) {
+      const int need = kDenseBytes + res.var_len;
+      enc_var(wd, code, nib, sh, res, eo, ro);
+      ENC_STAMP(4);
+      if (tid == 0) {
+        const bool fits = boff + need <= page_bytes;
+        sh.s_off = fits ? boff : -1;
+        n_spill += !fits;
+        if (fits) boff += need;
+      }
+    } else if (res.codes) {
       // first claim attempt in flight while the variable region is built
       const int need = kDenseBytes + res.var_len;
       int prev = -1;
@@ -686,6 +716,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
         ++n_enc;
       }
     }
+    if (kBlockMajor && tid == 0 && kvh == per - 1) *fill = boff;  // the block's records are placed
     ENC_STAMP(6);
     lds_barrier();  // sh (var32, s_off, s_ovf; rank on a head change) is reused by the next record
     ENC_STAMP(7);
@@ -1067,8 +1098,8 @@ extern "C" int fp_enc_trace_read(uint64_t* host, int64_t n) {
 }
 #endif
 
-extern "C" int fp_hbm_encode(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
-                             int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream) {
+static int encode_launch(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
+                         int64_t arena, int64_t page_bytes, int64_t max_close, bool ordered, fp_stream_t stream) {
   if (max_close == 0) return 0;
   if (check_store(d)) return -1;
   FP_CHECK(max_close > 0 && max_close <= d->list_cap, "close list too small");
@@ -1087,11 +1118,28 @@ extern "C" int fp_hbm_encode(const fp_store_t* d, const uint8_t* rank_of, int64_
     cus = n;
   }
   const int64_t records = max_close * 2 * d->kv_heads;
-  const int64_t grid = std::min<int64_t>(records, (int64_t)cus * kEncodeWgPerCu);
-  hipLaunchKernelGGL(encode_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
-                     reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+  if (ordered) {
+    const int64_t grid = std::min<int64_t>(max_close, (int64_t)cus * kEncodeWgPerCu);
+    hipLaunchKernelGGL(encode_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
+                       reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+  } else {
+    const int64_t grid = std::min<int64_t>(records, (int64_t)cus * kEncodeWgPerCu);
+    hipLaunchKernelGGL(encode_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
+                       reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+  }
   FP_LAUNCH_CHECK();
   return 0;
+}
+
+extern "C" int fp_hbm_encode(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
+                             int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream) {
+  return encode_launch(d, rank_of, rank_of_elems, layer, arena, page_bytes, max_close, false, stream);
+}
+
+extern "C" int fp_hbm_encode_ordered(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems,
+                                     int64_t layer, int64_t arena, int64_t page_bytes, int64_t max_close,
+                                     fp_stream_t stream) {
+  return encode_launch(d, rank_of, rank_of_elems, layer, arena, page_bytes, max_close, true, stream);
 }
 
 extern "C" int fp_hbm_commit(const fp_store_t* d, fp_stream_t stream) {

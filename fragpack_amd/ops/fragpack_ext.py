@@ -113,6 +113,7 @@ class Extension:
             "fp_hbm_prepare": [sp, _p, _i64, _p, _i64, _i64, _p],
             "fp_hbm_write": [sp, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p],
             "fp_hbm_encode": [sp, _p, _i64, _i64, _i64, _i64, _i64, _p],
+            "fp_hbm_encode_ordered": [sp, _p, _i64, _i64, _i64, _i64, _i64, _p],
             "fp_hbm_commit": [sp, _p],
             "fp_hbm_gather": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _p],
             "fp_hbm_export": [_p, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p],
@@ -218,7 +219,9 @@ class Extension:
                    _dev(value, "value"), value.stride(0), value.stride(1), _dev(slot_mapping, "slot_mapping"), n,
                    int(layer), _stream(key))
 
-    def hbm_encode(self, *args) -> None:
+    def hbm_encode(self, *args, ordered: bool = False) -> None:
+        """``ordered``: place each block's records in (kv, head) order
+        (fp_hbm_encode_ordered) instead of by arrival."""
         state, (rank_of, layer, arena, page_bytes, max_close) = args[:13], args[13:]
         if int(max_close) == 0:
             return
@@ -226,8 +229,8 @@ class Extension:
         _check(2 * int(max_close) <= state[6].numel(), "close list too small")
         _check(rank_of.numel() == d.num_layers * 2 * d.kv_heads * 256, "rank_of must hold every layer")
         _check(int(page_bytes) % 16 == 0 and int(page_bytes) < (1 << 31), "bad arena page size")
-        self._call("fp_hbm_encode", ctypes.byref(d), _dev(rank_of, "rank_of"), rank_of.numel(), int(layer),
-                   int(arena), int(page_bytes), int(max_close), _stream(rank_of))
+        self._call("fp_hbm_encode_ordered" if ordered else "fp_hbm_encode", ctypes.byref(d), _dev(rank_of, "rank_of"),
+                   rank_of.numel(), int(layer), int(arena), int(page_bytes), int(max_close), _stream(rank_of))
 
     def hbm_commit(self, *state) -> None:
         d = _store_desc(state)

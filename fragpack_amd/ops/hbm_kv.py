@@ -247,10 +247,16 @@ class HbmKvStore:
         """Store one layer's new K / V tokens (BF16 ``[N, H, 128]``) into staging."""
         extension().hbm_write(*self._state, key, value, slot_mapping, layer)
 
-    def encode(self, layer: int, max_close: int) -> None:
-        """Code this layer's records of every block closed this step."""
+    def encode(self, layer: int, max_close: int, ordered: bool = False) -> None:
+        """Code this layer's records of every block closed this step.
+
+        ``ordered``: place each block's records in (kv, head) order, so that
+        the arena bytes and which records spill depend only on the records
+        (the reference places them as they arrive).
+        """
         extension().hbm_encode(
-            *self._state, self.tables.rank_of, layer, self.arena_base[layer], self.arena_stride[layer], max_close
+            *self._state, self.tables.rank_of, layer, self.arena_base[layer], self.arena_stride[layer], max_close,
+            ordered=ordered,
         )
 
     def commit(self) -> None:

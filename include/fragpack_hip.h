@@ -124,6 +124,15 @@ int fp_hbm_write(const fp_store_t* s, const void* key, int64_t k_s0, int64_t k_s
 int fp_hbm_encode(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
                   int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream);
 
+/* fp_hbm_encode with placement by record order (SURVEY next item
+ * "deterministic page packing"; no counterpart in the reference, whose
+ * encode claims page space in arrival order, hbm_kv.cu:352-363): each closed
+ * block's 2H records are placed in (kv, head) order, a coded record taking
+ * the page's next bytes if they fit and spilling to the overflow pool if
+ * not, so the arena bytes and the spill set depend only on the records. */
+int fp_hbm_encode_ordered(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
+                          int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream);
+
 /* Release closed blocks' staging.  Replaces hbm_commit
  * (fragpack_ext.cpp:35-39, hbm_kv.cu:725-734). */
 int fp_hbm_commit(const fp_store_t* s, fp_stream_t stream);
