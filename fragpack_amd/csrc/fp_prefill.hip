@@ -218,6 +218,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
     store_tile(pf_smem, regs);
   }
   __syncthreads();
+  // Nothing in flight at the loop entry (Q and the first tile have landed):
+  // without this explicit wait the counter pass, merging the entry path,
+  // puts a vmcnt(0) before the first MFMA of every tile, i.e. waits for the
+  // next tile's loads right after issuing them.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = it * kPfKeys;
     const uint8_t* stage = pf_smem + (it & 1) * kStageBytes;
