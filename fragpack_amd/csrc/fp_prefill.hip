@@ -230,9 +230,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
     if (more) load_tile(p, page_of(key0 + kPfKeys), key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, regs);
 
     // ---- S^T = K Q^T: s[kt][qt], keys key0 + 16 kt + 4 q4 + r ----
+    // The tile runs in halves so that one half's exponentials overlap the
+    // other half's MFMAs within the wave: keys 0..31 are scored, then keys
+    // 32..63 are scored while P of keys 0..31 is formed (speculatively,
+    // against the running max); P of keys 32..63 is formed while the PV
+    // product of keys 0..31 runs.
+    //
+    // Scores stay unscaled (scale > 0 keeps the order); P = exp2(s c - m c)
+    // is one FMA and one exp per score.  The reference max m only moves when
+    // some column's max outgrows it by more than 2^kLazyMax (log2 domain), so
+    // O and l are rescaled on few tiles -- and only then is the speculative P
+    // of keys 0..31 recomputed; P <= 2^kLazyMax is exact enough in BF16 and
+    // fp32.
     pf_f32x4 s[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    auto qk = [&](int kt) {
       s[kt][0] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
       s[kt][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -241,23 +252,55 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
         s[kt][0] = pf_mfma(kf, qf[0][ks], s[kt][0]);
         s[kt][1] = pf_mfma(kf, qf[1][ks], s[kt][1]);
       }
-    }
-    // ---- mask, online softmax, P^T fragments ----
-    // Scores stay unscaled (scale > 0 keeps the order); P = exp2(s c - m c)
-    // is one FMA and one exp per score.  The reference max m only moves when
-    // some column's max outgrows it by more than 2^kLazyMax (log2 domain), so
-    // O and l are rescaled on few tiles; P <= 2^kLazyMax is exact enough in
-    // BF16 and fp32.
+    };
     // causal / length mask: only on tiles that reach some column's limit
     // (a wave-uniform branch; other tiles skip the compares)
-    if (__ballot(key0 + kPfKeys > min(kmax[0], kmax[1])) != 0) {
+    const bool mask_tile = __ballot(key0 + kPfKeys > min(kmax[0], kmax[1])) != 0;
+    auto mask = [&](int kt) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int r = 0; r < 4; ++r)
+          if (key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) s[kt][qt][r] = -INFINITY;
+    };
+    float e[4][2][4];
+    auto expo = [&](int kt, int qt, float nm) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) s[kt][qt][r] = -INFINITY;
+      for (int r = 0; r < 4; ++r) e[kt][qt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, nm));
+    };
+    auto neg_m = [&](int qt) { return m[qt] == -INFINITY ? 0.f : -m[qt] * p.scale_log2; };
+    qk(0);
+    qk(1);
+    if (mask_tile) {
+      mask(0);
+      mask(1);
+    }
+    // keys 32..63 scored in four k-steps; after each, four exponentials of
+    // keys 0..31 (pinned there: they run while the step's MFMAs execute)
+    {
+      const float nm0 = neg_m(0), nm1 = neg_m(1);
+      s[2][0] = s[2][1] = s[3][0] = s[3][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const uint4 k2 = *reinterpret_cast<const uint4*>(stage + (32 + j) * kKRow + 64 * ks + 16 * q4);
+        const uint4 k3 = *reinterpret_cast<const uint4*>(stage + (48 + j) * kKRow + 64 * ks + 16 * q4);
+        s[2][0] = pf_mfma(k2, qf[0][ks], s[2][0]);
+        s[2][1] = pf_mfma(k2, qf[1][ks], s[2][1]);
+        s[3][0] = pf_mfma(k3, qf[0][ks], s[3][0]);
+        s[3][1] = pf_mfma(k3, qf[1][ks], s[3][1]);
+        // exps (kt, qt) = (ks >> 1, ks & 1) of keys 0..31
+        const int kt = ks >> 1, qt = ks & 1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          e[kt][qt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, qt ? nm1 : nm0));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) asm volatile("" ::"v"(e[kt][qt][r]));  // not sunk into a later block
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (mask_tile) {
+      mask(2);
+      mask(3);
     }
     float mloc[2];
 #pragma unroll
@@ -282,43 +325,49 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
         l[qt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+        const float nm = neg_m(qt);
+        expo(0, qt, nm);
+        expo(1, qt, nm);
       }
     }
-    uint4 pf[2][2];  // [kk][qt]
+    // B operand of k-step kk: keys 32 kk + {4 q4 .. 4 q4 + 3} (tile 2 kk) and
+    // 32 kk + 16 + {4 q4 ..} (tile 2 kk + 1)
+    auto pfrag = [&](int kk, int qt) {
+      return make_uint4(pk_bf16(e[2 * kk][qt][0], e[2 * kk][qt][1]), pk_bf16(e[2 * kk][qt][2], e[2 * kk][qt][3]),
+                        pk_bf16(e[2 * kk + 1][qt][0], e[2 * kk + 1][qt][1]),
+                        pk_bf16(e[2 * kk + 1][qt][2], e[2 * kk + 1][qt][3]));
+    };
+    const uint4 p00 = pfrag(0, 0), p01 = pfrag(0, 1);
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const float nm = m[qt] == -INFINITY ? 0.f : -m[qt] * p.scale_log2;
-      float psum = 0.f;
-      float e[4][4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          e[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, nm));
-          psum += e[kt][r];
-        }
-      l[qt] += psum;
-      // B operand of k-step kk: keys 32 kk + {4 q4 .. 4 q4 + 3} (tile 2 kk) and
-      // 32 kk + 16 + {4 q4 ..} (tile 2 kk + 1)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        pf[kk][qt] = make_uint4(pk_bf16(e[2 * kk][0], e[2 * kk][1]), pk_bf16(e[2 * kk][2], e[2 * kk][3]),
-                                pk_bf16(e[2 * kk + 1][0], e[2 * kk + 1][1]), pk_bf16(e[2 * kk + 1][2], e[2 * kk + 1][3]));
+      const float nm = neg_m(qt);
+      expo(2, qt, nm);
+      expo(3, qt, nm);
     }
     // ---- O^T += V^T P^T: o[dt][qt], dims 16 dt + 4 q4 + r ----
     const uint8_t* vt = stage + kKBytes;
+    auto pv = [&](int kk, const uint4& pa, const uint4& pb) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint8_t* vrow = vt + (16 * dt + j) * kVRow;
-      const int sw = (2 * dt + (j >> 3)) & 15;  // (row >> 3) & 15
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint8_t* vrow = vt + (16 * dt + j) * kVRow;
+        const int sw = (2 * dt + (j >> 3)) & 15;  // (row >> 3) & 15
         const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 8 * ((8 * kk + q4) ^ sw));
         const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8 * ((8 * kk + 4 + q4) ^ sw));
         const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        o[dt][0] = pf_mfma(vf, pf[kk][0], o[dt][0]);
-        o[dt][1] = pf_mfma(vf, pf[kk][1], o[dt][1]);
+        o[dt][0] = pf_mfma(vf, pa, o[dt][0]);
+        o[dt][1] = pf_mfma(vf, pb, o[dt][1]);
       }
+    };
+    pv(0, p00, p01);
+    pv(1, pfrag(1, 0), pfrag(1, 1));
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float psum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) psum += e[kt][qt][r];
+      l[qt] += psum;
     }
     if (more) store_tile(pf_smem + ((it + 1) & 1) * kStageBytes, regs);
     __syncthreads();
