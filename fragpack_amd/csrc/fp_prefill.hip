@@ -41,15 +41,17 @@ typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kPfRows = 128;       // query rows (token x head) per workgroup
 constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfDim = 128;
-constexpr int kKRow = 272;         // LDS bytes per K row (256 + 16 pad)
+// K rows of 256 bytes whose 16-byte chunks are XOR-swizzled by the row
+// (chunk c of row r at slot c ^ (r & 15)): the fragment reads of 16
+// consecutive rows then cover all banks.
+constexpr int kKRow = 256;
 // V^T rows of 144 bytes with the 8-byte key blocks of row d stored at block
 // index kb ^ ((d >> 3) & 15): both the transposing writes and the fragment
 // reads then spread over all banks (unswizzled 136-byte rows put eight lanes
 // of every transposing write on the same banks).
 constexpr int kVRow = 144;
-constexpr int kKBytes = kPfKeys * kKRow;   // 17408
+constexpr int kKBytes = kPfKeys * kKRow;   // 16384
 constexpr int kVBytes = kPfDim * kVRow;    // 17408
-constexpr int kStageBytes = kKBytes + kVBytes;
 constexpr float kLazyMax = 8.f;  // log2 headroom of the softmax reference max
 
 struct PrefillParams {
@@ -86,11 +88,10 @@ __device__ __forceinline__ uint32_t pf_perm(uint32_t hi, uint32_t lo, uint32_t s
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Global -> register staging of one 64-key tile: thread t holds K chunks
-// (key 16i + t / 16, dims 8 (t % 16) ..) and V chunks (keys 4 (t / 16) + i,
-// same dims), i = 0..3.
+// Global -> register staging of one 64-key V tile: thread t holds the
+// chunks (keys 4 (t / 16) + i, dims 8 (t % 16) ..), i = 0..3.  (K goes
+// straight to LDS.)
 struct TileRegs {
-  uint4 k[4];
   uint4 v[4];
 };
 
@@ -113,29 +114,36 @@ __device__ __forceinline__ uint4 pf_bld16(pf_rsrc_t r, int off) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef __attribute__((address_space(3))) void* pf_lds_ptr_t;
+
+// Starts a 64-key tile's loads: K straight into the stage's K area with
+// buffer_load ... lds (each wave instruction fills 1 KB = four rows; lane L
+// of rows 4 i' .. fetches the chunk that belongs at slot L % 16 of row
+// L / 16, i.e. chunk (L % 16) ^ (row & 15); rows past the tile read zero),
+// V into registers.
 __device__ __forceinline__ void load_tile(const PrefillParams& p, int64_t page, int key0, int nkeys, int h,
-                                          TileRegs& r) {
+                                          uint8_t* kst, TileRegs& r) {
   const int t = threadIdx.x;
+  const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int dc = t & 15;
   const int row = p.kvh * kPfDim * 2;  // bytes between consecutive keys
   const pf_rsrc_t rk = tile_rsrc(p.wk, page, key0, nkeys, h, p.kvh);
   const pf_rsrc_t rv = tile_rsrc(p.wv, page, key0, nkeys, h, p.kvh);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    r.k[i] = pf_bld16(rk, (16 * i + (t >> 4)) * row + 16 * dc);
-    r.v[i] = pf_bld16(rv, (4 * (t >> 4) + i) * row + 16 * dc);
+    const int kr = 16 * w + 4 * i + (lane >> 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pf_lds_ptr_t)(kst + (16 * w + 4 * i) * kKRow), 16,
+                                             kr * row + 16 * ((lane & 15) ^ (kr & 15)), 0, 0, 0);
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.v[i] = pf_bld16(rv, (4 * (t >> 4) + i) * row + 16 * dc);
 }
 
-// Registers -> LDS stage: K rows as they are, V transposed (8-byte writes of
-// four consecutive keys of one dim).
-__device__ __forceinline__ void store_tile(uint8_t* stage, const TileRegs& r) {
+// Registers -> LDS stage: V transposed (8-byte writes of four consecutive
+// keys of one dim).
+__device__ __forceinline__ void store_tile(uint8_t* vt, const TileRegs& r) {
   const int t = threadIdx.x;
   const int dc = t & 15;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<uint4*>(stage + (16 * i + (t >> 4)) * kKRow + 16 * dc) = r.k[i];
-  uint8_t* vt = stage + kKBytes;
   const int kg = t >> 4;  // keys 4 kg .. 4 kg + 3
   auto dw = [&](int i, int e) { return e == 0 ? r.v[i].x : e == 1 ? r.v[i].y : e == 2 ? r.v[i].z : r.v[i].w; };
 #pragma unroll
@@ -151,7 +159,16 @@ __device__ __forceinline__ void store_tile(uint8_t* stage, const TileRegs& r) {
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillParams p) {
-  extern __shared__ __align__(16) uint8_t pf_smem[];
+  // K stages are two separate LDS objects and each trip of the tile loop
+  // below names them statically: the counter pass then sees that the next
+  // tile's K transfer into one cannot alias this tile's reads of the other
+  // (one LDS object with computed stage offsets makes every K read wait for
+  // the transfer just issued).  The V stages likewise: reads of the dynamic
+  // LDS block are not known to miss the K objects.
+  __shared__ __align__(16) uint8_t pf_k0[kKBytes];
+  __shared__ __align__(16) uint8_t pf_k1[kKBytes];
+  __shared__ __align__(16) uint8_t pf_v0[kVBytes];
+  __shared__ __align__(16) uint8_t pf_v1[kVBytes];
   const int h = blockIdx.y;
   // longest query tiles first: later tiles see more keys under the causal mask
   const int b = blockIdx.x % p.num_seqs;
@@ -214,8 +231,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
   };
   TileRegs regs;
   if (ntiles > 0) {
-    load_tile(p, page_of(0), 0, min(kPfKeys, kend), h, regs);
-    store_tile(pf_smem, regs);
+    load_tile(p, page_of(0), 0, min(kPfKeys, kend), h, pf_k0, regs);
+    store_tile(pf_v0, regs);
   }
   __syncthreads();
   // Nothing in flight at the loop entry (Q and the first tile have landed):
@@ -223,11 +240,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
   // puts a vmcnt(0) before the first MFMA of every tile, i.e. waits for the
   // next tile's loads right after issuing them.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  for (int it = 0; it < ntiles; ++it) {
+  auto tile = [&](int it, const uint8_t* stage, uint8_t* knext, const uint8_t* vstage, uint8_t* vnext)
+                  __attribute__((always_inline)) {
     const int key0 = it * kPfKeys;
-    const uint8_t* stage = pf_smem + (it & 1) * kStageBytes;
     const bool more = it + 1 < ntiles;
-    if (more) load_tile(p, page_of(key0 + kPfKeys), key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, regs);
+    if (more)
+      load_tile(p, page_of(key0 + kPfKeys), key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, knext, regs);
 
     // ---- S^T = K Q^T: s[kt][qt], keys key0 + 16 kt + 4 q4 + r ----
     // The tile runs in halves so that one half's exponentials overlap the
@@ -248,7 +266,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
       s[kt][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(stage + (16 * kt + j) * kKRow + 64 * ks + 16 * q4);
+        const uint4 kf = *reinterpret_cast<const uint4*>(stage + (16 * kt + j) * kKRow + 16 * ((4 * ks + q4) ^ j));
         s[kt][0] = pf_mfma(kf, qf[0][ks], s[kt][0]);
         s[kt][1] = pf_mfma(kf, qf[1][ks], s[kt][1]);
       }
@@ -282,8 +300,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
       s[2][0] = s[2][1] = s[3][0] = s[3][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const uint4 k2 = *reinterpret_cast<const uint4*>(stage + (32 + j) * kKRow + 64 * ks + 16 * q4);
-        const uint4 k3 = *reinterpret_cast<const uint4*>(stage + (48 + j) * kKRow + 64 * ks + 16 * q4);
+        const uint4 k2 = *reinterpret_cast<const uint4*>(stage + (32 + j) * kKRow + 16 * ((4 * ks + q4) ^ j));
+        const uint4 k3 = *reinterpret_cast<const uint4*>(stage + (48 + j) * kKRow + 16 * ((4 * ks + q4) ^ j));
         s[2][0] = pf_mfma(k2, qf[0][ks], s[2][0]);
         s[2][1] = pf_mfma(k2, qf[1][ks], s[2][1]);
         s[3][0] = pf_mfma(k3, qf[0][ks], s[3][0]);
@@ -345,7 +363,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
       expo(3, qt, nm);
     }
     // ---- O^T += V^T P^T: o[dt][qt], dims 16 dt + 4 q4 + r ----
-    const uint8_t* vt = stage + kKBytes;
+    const uint8_t* vt = vstage;
     auto pv = [&](int kk, const uint4& pa, const uint4& pb) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
@@ -369,8 +387,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
         for (int r = 0; r < 4; ++r) psum += e[kt][qt][r];
       l[qt] += psum;
     }
-    if (more) store_tile(pf_smem + ((it + 1) & 1) * kStageBytes, regs);
+    if (more) store_tile(vnext, regs);
     __syncthreads();
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    tile(it, pf_k0, pf_k1, pf_v0, pf_v1);
+    if (it + 1 < ntiles) tile(it + 1, pf_k1, pf_k0, pf_v1, pf_v0);
   }
   // ---- normalise and store: lane holds dims 16 dt + 4 q4 + r of query j ----
 #pragma unroll
@@ -431,12 +453,8 @@ extern "C" int fp_prefill_attention(const void* q, int64_t q_stride, const void*
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   p.causal = causal ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // two 34 KB stages exceed the default 64 KB dynamic LDS limit
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
-  FP_CHECK(attr == hipSuccess, "cannot raise the prefill kernel's LDS limit");
-  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(tiles * num_seqs), (unsigned)kv_heads), dim3(256),
-                     2 * kStageBytes, s, p);
+  // all LDS is static (two K and two V stages, 66 KB)
+  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(tiles * num_seqs), (unsigned)kv_heads), dim3(256), 0, s, p);
   FP_LAUNCH_CHECK();
   return 0;
 }
