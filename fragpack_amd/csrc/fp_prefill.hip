@@ -41,17 +41,11 @@ typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kPfRows = 128;       // query rows (token x head) per workgroup
 constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfDim = 128;
-// K rows of 256 bytes whose 16-byte chunks are XOR-swizzled by the row
-// (chunk c of row r at slot c ^ (r & 15)): the fragment reads of 16
-// consecutive rows then cover all banks.
+// K and V tiles in LDS: key-major rows of 256 bytes whose 16-byte chunks
+// are XOR-swizzled by the row (chunk c of row r at slot c ^ (r & 15)), so
+// the fragment reads of 16 consecutive rows cover all banks.
 constexpr int kKRow = 256;
-// V^T rows of 144 bytes with the 8-byte key blocks of row d stored at block
-// index kb ^ ((d >> 3) & 15): both the transposing writes and the fragment
-// reads then spread over all banks (unswizzled 136-byte rows put eight lanes
-// of every transposing write on the same banks).
-constexpr int kVRow = 144;
-constexpr int kKBytes = kPfKeys * kKRow;   // 16384
-constexpr int kVBytes = kPfDim * kVRow;    // 17408
+constexpr int kKBytes = kPfKeys * kKRow;   // 16384 (K or V)
 constexpr float kLazyMax = 8.f;  // log2 headroom of the softmax reference max
 
 struct PrefillParams {
@@ -88,74 +82,47 @@ __device__ __forceinline__ uint32_t pf_perm(uint32_t hi, uint32_t lo, uint32_t s
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Global -> register staging of one 64-key V tile: thread t holds the
-// chunks (keys 4 (t / 16) + i, dims 8 (t % 16) ..), i = 0..3.  (K goes
-// straight to LDS.)
-struct TileRegs {
-  uint4 v[4];
-};
-
 typedef __amdgpu_buffer_rsrc_t pf_rsrc_t;
-typedef uint32_t pf_u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* pf_lds_ptr_t;
 
 // A 64-key tile lies in one 128-token page (tiles start at multiples of 64):
-// rows key0 .. key0 + nkeys - 1 of head h are ``row`` bytes apart from the
-// tile's first row; a buffer resource over exactly those rows reads zero
-// past them.
-__device__ __forceinline__ pf_rsrc_t tile_rsrc(const uint16_t* base, int64_t page, int key0, int nkeys, int h,
-                                               int kvh) {
+// rows key0 .. key0 + 63 of head h are ``kvh * 256`` bytes apart, starting
+// at the tile's first row.
+__device__ __forceinline__ pf_rsrc_t tile_rsrc(const uint16_t* base, int64_t page, int key0, int h, int kvh) {
   const uint16_t* first = base + ((page * 128 + (key0 & 127)) * kvh + h) * kPfDim;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(first), (short)0, nkeys * kvh * kPfDim * 2,
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(first), (short)0, 64 * kvh * kPfDim * 2,
                                            0x00020000);
 }
 
-__device__ __forceinline__ uint4 pf_bld16(pf_rsrc_t r, int off) {
-  const pf_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-typedef __attribute__((address_space(3))) void* pf_lds_ptr_t;
-
-// Starts a 64-key tile's loads: K straight into the stage's K area with
-// buffer_load ... lds (each wave instruction fills 1 KB = four rows; lane L
-// of rows 4 i' .. fetches the chunk that belongs at slot L % 16 of row
-// L / 16, i.e. chunk (L % 16) ^ (row & 15); rows past the tile read zero),
-// V into registers.
+// Loads a 64-key tile of K and of V straight into LDS (buffer_load ... lds):
+// rows of 256 bytes, 16-byte chunk c of row r at slot c ^ (r & 15).  Each
+// wave instruction fills 1 KB = four rows, lane L the slot L % 16 of row
+// L / 16, so lane L fetches chunk (L % 16) ^ (row & 15).  Rows past the
+// tile's ``nkeys`` repeat its last row: V rows stay finite (their P is 0)
+// and every load stays inside the page.
 __device__ __forceinline__ void load_tile(const PrefillParams& p, int64_t page, int key0, int nkeys, int h,
-                                          uint8_t* kst, TileRegs& r) {
-  const int t = threadIdx.x;
-  const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int dc = t & 15;
+                                          uint8_t* kst, uint8_t* vst) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = p.kvh * kPfDim * 2;  // bytes between consecutive keys
-  const pf_rsrc_t rk = tile_rsrc(p.wk, page, key0, nkeys, h, p.kvh);
-  const pf_rsrc_t rv = tile_rsrc(p.wv, page, key0, nkeys, h, p.kvh);
+  const pf_rsrc_t rk = tile_rsrc(p.wk, page, key0, h, p.kvh);
+  const pf_rsrc_t rv = tile_rsrc(p.wv, page, key0, h, p.kvh);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int kr = 16 * w + 4 * i + (lane >> 4);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pf_lds_ptr_t)(kst + (16 * w + 4 * i) * kKRow), 16,
-                                             kr * row + 16 * ((lane & 15) ^ (kr & 15)), 0, 0, 0);
+    const int r = 16 * w + 4 * i + (lane >> 4);
+    const int off = min(r, nkeys - 1) * row + 16 * ((lane & 15) ^ (r & 15));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pf_lds_ptr_t)(kst + (16 * w + 4 * i) * kKRow), 16, off, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pf_lds_ptr_t)(vst + (16 * w + 4 * i) * kKRow), 16, off, 0, 0, 0);
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = pf_bld16(rv, (4 * (t >> 4) + i) * row + 16 * dc);
 }
 
-// Registers -> LDS stage: V transposed (8-byte writes of four consecutive
-// keys of one dim).
-__device__ __forceinline__ void store_tile(uint8_t* vt, const TileRegs& r) {
-  const int t = threadIdx.x;
-  const int dc = t & 15;
-  const int kg = t >> 4;  // keys 4 kg .. 4 kg + 3
-  auto dw = [&](int i, int e) { return e == 0 ? r.v[i].x : e == 1 ? r.v[i].y : e == 2 ? r.v[i].z : r.v[i].w; };
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t a = dw(0, e), b = dw(1, e), c = dw(2, e), d = dw(3, e);
-    // dims 8 dc + 2e (low halves) and 8 dc + 2e + 1 (high halves)
-    const uint2 lo = make_uint2(pf_perm(b, a, 0x05040100u), pf_perm(d, c, 0x05040100u));
-    const uint2 hi = make_uint2(pf_perm(b, a, 0x07060302u), pf_perm(d, c, 0x07060302u));
-    // rows 8 dc + 2 e (+ 1): (d >> 3) & 15 = dc
-    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e) * kVRow + 8 * (kg ^ dc)) = lo;
-    *reinterpret_cast<uint2*>(vt + (8 * dc + 2 * e + 1) * kVRow + 8 * (kg ^ dc)) = hi;
-  }
+typedef short pf_i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i receives
+// element i % 4 of the 8-byte pieces addressed by lanes 4 e + i / 4,
+// e = 0..3 -- a 4 x 4 transpose of 16-bit elements across lanes.
+__device__ __forceinline__ uint2 lds_tr16(const uint8_t* a) {
+  const pf_i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) pf_i16x4*)a);
+  return __builtin_bit_cast(uint2, v);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillParams p) {
@@ -167,8 +134,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
   // LDS block are not known to miss the K objects.
   __shared__ __align__(16) uint8_t pf_k0[kKBytes];
   __shared__ __align__(16) uint8_t pf_k1[kKBytes];
-  __shared__ __align__(16) uint8_t pf_v0[kVBytes];
-  __shared__ __align__(16) uint8_t pf_v1[kVBytes];
+  __shared__ __align__(16) uint8_t pf_v0[kKBytes];
+  __shared__ __align__(16) uint8_t pf_v1[kKBytes];
   const int h = blockIdx.y;
   // longest query tiles first: later tiles see more keys under the causal mask
   const int b = blockIdx.x % p.num_seqs;
@@ -229,23 +196,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
     }
     return __builtin_amdgcn_readlane(pages, pi & 63);
   };
-  TileRegs regs;
-  if (ntiles > 0) {
-    load_tile(p, page_of(0), 0, min(kPfKeys, kend), h, pf_k0, regs);
-    store_tile(pf_v0, regs);
-  }
+  if (ntiles > 0) load_tile(p, page_of(0), 0, min(kPfKeys, kend), h, pf_k0, pf_v0);
   __syncthreads();
   // Nothing in flight at the loop entry (Q and the first tile have landed):
   // without this explicit wait the counter pass, merging the entry path,
   // puts a vmcnt(0) before the first MFMA of every tile, i.e. waits for the
   // next tile's loads right after issuing them.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // V fragment lanes: row x = 4 q4 + j / 4 of each 16-row block, byte
+  // 8 (j & 1) of the chunk; the chunk's slot term 16 ((j >> 1 & 1) ^ x)
+  const int vx = 4 * q4 + (j >> 2);
+  const int vlane = vx * kKRow + 8 * (j & 1), vsw = 16 * (((j >> 1) & 1) ^ vx);
   auto tile = [&](int it, const uint8_t* stage, uint8_t* knext, const uint8_t* vstage, uint8_t* vnext)
                   __attribute__((always_inline)) {
     const int key0 = it * kPfKeys;
     const bool more = it + 1 < ntiles;
     if (more)
-      load_tile(p, page_of(key0 + kPfKeys), key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, knext, regs);
+      load_tile(p, page_of(key0 + kPfKeys), key0 + kPfKeys, min(kPfKeys, kend - key0 - kPfKeys), h, knext, vnext);
 
     // ---- S^T = K Q^T: s[kt][qt], keys key0 + 16 kt + 4 q4 + r ----
     // The tile runs in halves so that one half's exponentials overlap the
@@ -363,14 +330,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
       expo(3, qt, nm);
     }
     // ---- O^T += V^T P^T: o[dt][qt], dims 16 dt + 4 q4 + r ----
-    const uint8_t* vt = vstage;
+    // V^T fragment (dims 16 dt + j, keys 32 kk + {4 q4 .. 4 q4 + 3} and
+    // 32 kk + 16 + {4 q4 ..}) by two transposing reads: lane (s = j, g = q4)
+    // addresses row 32 kk (+ 16) + 4 g + s / 4, dims 16 dt + 4 (s % 4) ..,
+    // so lane j receives dim 16 dt + j of rows 32 kk (+ 16) + 4 g + e.
     auto pv = [&](int kk, const uint4& pa, const uint4& pb) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint8_t* vrow = vt + (16 * dt + j) * kVRow;
-        const int sw = (2 * dt + (j >> 3)) & 15;  // (row >> 3) & 15
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 8 * ((8 * kk + q4) ^ sw));
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8 * ((8 * kk + 4 + q4) ^ sw));
+        // chunk 2 dt + (j >> 1 & 1) of row x = 4 q4 + j / 4 (mod 16) sits at
+        // slot chunk ^ x
+        const uint8_t* base = vstage + (vsw ^ (32 * dt)) + vlane;
+        const uint2 lo = lds_tr16(base + 32 * kk * kKRow);
+        const uint2 hi = lds_tr16(base + (32 * kk + 16) * kKRow);
         const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
         o[dt][0] = pf_mfma(vf, pa, o[dt][0]);
         o[dt][1] = pf_mfma(vf, pb, o[dt][1]);
@@ -387,7 +358,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) p
         for (int r = 0; r < 4; ++r) psum += e[kt][qt][r];
       l[qt] += psum;
     }
-    if (more) store_tile(vnext, regs);
     __syncthreads();
   };
   for (int it = 0; it < ntiles; it += 2) {
@@ -453,7 +423,7 @@ extern "C" int fp_prefill_attention(const void* q, int64_t q_stride, const void*
   p.scale_log2 = (float)(scale * 1.4426950408889634);
   p.causal = causal ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // all LDS is static (two K and two V stages, 66 KB)
+  // all LDS is static (two K and two V stages, 64 KB)
   hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(tiles * num_seqs), (unsigned)kv_heads), dim3(256), 0, s, p);
   FP_LAUNCH_CHECK();
   return 0;
