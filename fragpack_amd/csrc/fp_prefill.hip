@@ -11,13 +11,15 @@
 // bottom-right: query i sees keys j <= i + seqused_k - q_len).
 //
 // Design (MI355X):
-// * One 256-thread workgroup (4 wavefronts) per (128-row query tile, KV head).
-//   The 128 rows are T = 128 / G tokens x G query heads of the KV head
-//   (head-major), so every K / V tile read from HBM serves the whole GQA
-//   group.  Wave w owns rows 32w .. 32w + 31 as two 16-column MFMA tiles.
-// * Keys stream in 64-key tiles through double-buffered LDS: K row-major
-//   (padded rows), V transposed to [dim][key] on the way in, so both MFMA
-//   A operands are contiguous LDS reads.
+// * One 512-thread workgroup (8 wavefronts) per (256-row query tile, KV head).
+//   The 256 rows are T = 256 / G tokens x G query heads of the KV head
+//   (head-major), so every K / V tile read serves the whole GQA group and
+//   eight waves.  Wave w owns rows 32w .. 32w + 31 as two 16-column MFMA
+//   tiles.
+// * Keys stream in 64-key tiles through double-buffered LDS, K and V both
+//   key-major and loaded straight from HBM into LDS (buffer_load ... lds, no
+//   registers).  K fragments are plain 16-byte reads; V^T fragments come
+//   from ds_read_b64_tr_b16 transposing reads.
 // * S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_16x16x32_bf16.  The
 //   accumulator layout of S^T (lane = query column, 4 consecutive keys per
 //   16-lane group) is, after BF16 packing, exactly the B operand of the PV
@@ -38,7 +40,9 @@ namespace {
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPfRows = 128;       // query rows (token x head) per workgroup
+constexpr int kPfWaves = 8;        // wavefronts per workgroup, 32 query rows each
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = 32 * kPfWaves;  // query rows (token x head) per workgroup
 constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfDim = 128;
 // K and V tiles in LDS: key-major rows of 256 bytes whose 16-byte chunks
@@ -106,12 +110,13 @@ __device__ __forceinline__ void load_tile(const PrefillParams& p, int64_t page, 
   const int row = p.kvh * kPfDim * 2;  // bytes between consecutive keys
   const pf_rsrc_t rk = tile_rsrc(p.wk, page, key0, h, p.kvh);
   const pf_rsrc_t rv = tile_rsrc(p.wv, page, key0, h, p.kvh);
+  constexpr int kRows = kPfKeys / kPfWaves;  // rows per wave, four per instruction
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * w + 4 * i + (lane >> 4);
+  for (int i = 0; i < kRows / 4; ++i) {
+    const int r0 = kRows * w + 4 * i, r = r0 + (lane >> 4);
     const int off = min(r, nkeys - 1) * row + 16 * ((lane & 15) ^ (r & 15));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pf_lds_ptr_t)(kst + (16 * w + 4 * i) * kKRow), 16, off, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pf_lds_ptr_t)(vst + (16 * w + 4 * i) * kKRow), 16, off, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pf_lds_ptr_t)(kst + r0 * kKRow), 16, off, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pf_lds_ptr_t)(vst + r0 * kKRow), 16, off, 0, 0, 0);
   }
 }
 
@@ -125,7 +130,7 @@ __device__ __forceinline__ uint2 lds_tr16(const uint8_t* a) {
   return __builtin_bit_cast(uint2, v);
 }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillParams p) {
   // K stages are two separate LDS objects and each trip of the tile loop
   // below names them statically: the counter pass then sees that the next
   // tile's K transfer into one cannot alias this tile's reads of the other
@@ -424,7 +429,7 @@ extern "C" int fp_prefill_attention(const void* q, int64_t q_stride, const void*
   p.causal = causal ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // all LDS is static (two K and two V stages, 64 KB)
-  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(tiles * num_seqs), (unsigned)kv_heads), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(tiles * num_seqs), (unsigned)kv_heads), dim3(kPfThreads), 0, s, p);
   FP_LAUNCH_CHECK();
   return 0;
 }
