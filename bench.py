@@ -369,6 +369,32 @@ def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int
     return res
 
 
+def hbm_ceilings(torch) -> dict:
+    """Plain device-wide read, copy and fill rates on this box (torch kernels
+    over 8 GB / 4 GB buffers): the practical HBM ceilings the decode and
+    encode rates are read against, beside the 8 TB/s peak."""
+    n = 8 << 30
+    x = torch.ones(n // 8, dtype=torch.int64, device="cuda")
+    y = torch.empty(n // 16, dtype=torch.int64, device="cuda")
+    out = {}
+    for name, fn, nbytes in (("read_GBps", lambda: x.sum(), n), ("copy_GBps", lambda: y.copy_(x[: n // 16]), n),
+                             ("write_GBps", lambda: y.fill_(3), n // 2)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(nbytes / (e0.elapsed_time(e1) / 10) / 1e6, 1)  # copy: bytes read + written
+    del x, y
+    torch.cuda.empty_cache()
+    log(f"HBM ceilings: {out}")
+    return out
+
+
 def cpu_baseline(torch, res, args) -> dict:
     """The CPU oracle (C, OpenMP) on the same decode step: decode every record
     of the 4 x 8192-token layer and run fp32 attention, timed on this host's
@@ -443,6 +469,7 @@ def main() -> None:
     ap.add_argument("--large-steps", type=int, default=20)
     ap.add_argument("--no-layer-step", action="store_true",
                     help="skip the per-layer serving step legs (write, attention, encode)")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the plain read / copy / fill rate legs")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the batch-64 context sweep (8K and 16K, both arms) beside config 4's 32K")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -525,6 +552,8 @@ def main() -> None:
                           "bf16_paged_us_per_step": round(arms[1]["step_ms"] * 1e3, 1),
                           "compressed_step_speedup": round(arms[1]["step_ms"] / arms[0]["step_ms"], 3),
                           "validated": arms[0]["valid"] and arms[1]["valid"]})
+    torch.cuda.empty_cache()
+    ceil = None if args.no_ceilings else hbm_ceilings(torch)
     step_s = res["step_ms"] / 1e3
     kern_s = res["kern_ms"] / 1e3
     achieved = res["algo_bytes"] / kern_s / 1e9
@@ -607,6 +636,12 @@ def main() -> None:
                                          "us": round(enc_ordered["ms"] * 1e3, 1),
                                          "effective_GBps": round(enc_ordered["eff_bytes"] / enc_ordered["ms"] / 1e6, 1),
                                          "fallbacks": enc_ordered["fallbacks"], "spills": enc_ordered["spills"]}
+    if ceil is not None:
+        line["hbm_ceilings"] = ceil
+        if large is not None:
+            line["decode_large"]["frac_of_read_ceiling"] = round(la / ceil["read_GBps"], 4)
+        if enc is not None:
+            line["encode"]["frac_of_copy_ceiling"] = round(enc["read_write_bytes"] / enc["ms"] / 1e6 / ceil["copy_GBps"], 4)
     print(json.dumps(line))
 
 
