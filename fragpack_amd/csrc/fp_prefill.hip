@@ -40,9 +40,11 @@ namespace {
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPfWaves = 8;        // wavefronts per workgroup, 32 query rows each
+constexpr int kPfQt = 2;           // 16-row query tiles per wavefront
+constexpr int kPfWaves = 8;        // wavefronts per workgroup
+constexpr int kPfWavesPerEu = 2;
 constexpr int kPfThreads = 64 * kPfWaves;
-constexpr int kPfRows = 32 * kPfWaves;  // query rows (token x head) per workgroup
+constexpr int kPfRows = 16 * kPfQt * kPfWaves;  // query rows (token x head) per workgroup
 constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfDim = 128;
 // K and V tiles in LDS: key-major rows of 256 bytes whose 16-byte chunks
@@ -130,7 +132,7 @@ __device__ __forceinline__ uint2 lds_tr16(const uint8_t* a) {
   return __builtin_bit_cast(uint2, v);
 }
 
-__global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEu))) prefill_kernel(PrefillParams p) {
   // K stages are two separate LDS objects and each trip of the tile loop
   // below names them statically: the counter pass then sees that the next
   // tile's K transfer into one cannot alias this tile's reads of the other
@@ -155,21 +157,21 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, q4 = lane >> 4;
-  // this lane's two query columns (tiles qt = 0, 1): row -> (head g, token t)
-  int tok[2], hq[2];
-  bool rvalid[2];
+  // this lane's query columns (tiles qt): row -> (head g, token t)
+  int tok[kPfQt], hq[kPfQt];
+  bool rvalid[kPfQt];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int row = 32 * w + 16 * qt + j;
+  for (int qt = 0; qt < kPfQt; ++qt) {
+    const int row = 16 * kPfQt * w + 16 * qt + j;
     const int g = row / T, t = row - g * T;
     tok[qt] = t0 + t;
     hq[qt] = h * p.group + g;
     rvalid[qt] = tok[qt] < qlen;
   }
   // Q^T fragments (B operands): lane (j, q4) holds dims 32 ks + 8 q4 .. + 7
-  uint4 qf[2][4];
+  uint4 qf[kPfQt][4];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < kPfQt; ++qt) {
     const uint16_t* qrow = p.q + (int64_t)(q0 + (rvalid[qt] ? tok[qt] : 0)) * p.q_stride + (int64_t)hq[qt] * kPfDim;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -180,16 +182,21 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
   const int kend = p.causal ? min(klen, last_tok + shift + 1) : klen;
   const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
   // causal limit per query column
-  int kmax[2];
+  int kmax[kPfQt];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) kmax[qt] = p.causal ? min(klen, tok[qt] + shift + 1) : klen;
+  for (int qt = 0; qt < kPfQt; ++qt) kmax[qt] = p.causal ? min(klen, tok[qt] + shift + 1) : klen;
 
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  pf_f32x4 o[8][2];
+  float m[kPfQt], l[kPfQt];
+#pragma unroll
+  for (int qt = 0; qt < kPfQt; ++qt) {
+    m[qt] = -INFINITY;
+    l[qt] = 0.f;
+  }
+  pf_f32x4 o[8][kPfQt];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qt = 0; qt < kPfQt; ++qt) o[dt][qt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 
   // page ids of the tiles: lane j holds block_table entry 64 pb + j
   int pages = 0, pbase = -1;
@@ -232,28 +239,31 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
     // O and l are rescaled on few tiles -- and only then is the speculative P
     // of keys 0..31 recomputed; P <= 2^kLazyMax is exact enough in BF16 and
     // fp32.
-    pf_f32x4 s[4][2];
+    pf_f32x4 s[4][kPfQt];
     auto qk = [&](int kt) {
-      s[kt][0] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
-      s[kt][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int qt = 0; qt < kPfQt; ++qt) s[kt][qt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const uint4 kf = *reinterpret_cast<const uint4*>(stage + (16 * kt + j) * kKRow + 16 * ((4 * ks + q4) ^ j));
-        s[kt][0] = pf_mfma(kf, qf[0][ks], s[kt][0]);
-        s[kt][1] = pf_mfma(kf, qf[1][ks], s[kt][1]);
+#pragma unroll
+        for (int qt = 0; qt < kPfQt; ++qt) s[kt][qt] = pf_mfma(kf, qf[qt][ks], s[kt][qt]);
       }
     };
     // causal / length mask: only on tiles that reach some column's limit
     // (a wave-uniform branch; other tiles skip the compares)
-    const bool mask_tile = __ballot(key0 + kPfKeys > min(kmax[0], kmax[1])) != 0;
+    int kmin = kmax[0];
+#pragma unroll
+    for (int qt = 1; qt < kPfQt; ++qt) kmin = min(kmin, kmax[qt]);
+    const bool mask_tile = __ballot(key0 + kPfKeys > kmin) != 0;
     auto mask = [&](int kt) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int qt = 0; qt < kPfQt; ++qt)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (key0 + 16 * kt + 4 * q4 + r >= kmax[qt]) s[kt][qt][r] = -INFINITY;
     };
-    float e[4][2][4];
+    float e[4][kPfQt][4];
     auto expo = [&](int kt, int qt, float nm) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) e[kt][qt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, nm));
@@ -265,26 +275,35 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
       mask(0);
       mask(1);
     }
-    // keys 32..63 scored in four k-steps; after each, four exponentials of
-    // keys 0..31 (pinned there: they run while the step's MFMAs execute)
+    // keys 32..63 scored in four k-steps; after each, a quarter of the
+    // exponentials of keys 0..31 (pinned there: they run while the step's
+    // MFMAs execute)
     {
-      const float nm0 = neg_m(0), nm1 = neg_m(1);
-      s[2][0] = s[2][1] = s[3][0] = s[3][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+      float nm[kPfQt];
+#pragma unroll
+      for (int qt = 0; qt < kPfQt; ++qt) {
+        nm[qt] = neg_m(qt);
+        s[2][qt] = s[3][qt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const uint4 k2 = *reinterpret_cast<const uint4*>(stage + (32 + j) * kKRow + 16 * ((4 * ks + q4) ^ j));
         const uint4 k3 = *reinterpret_cast<const uint4*>(stage + (48 + j) * kKRow + 16 * ((4 * ks + q4) ^ j));
-        s[2][0] = pf_mfma(k2, qf[0][ks], s[2][0]);
-        s[2][1] = pf_mfma(k2, qf[1][ks], s[2][1]);
-        s[3][0] = pf_mfma(k3, qf[0][ks], s[3][0]);
-        s[3][1] = pf_mfma(k3, qf[1][ks], s[3][1]);
-        // exps (kt, qt) = (ks >> 1, ks & 1) of keys 0..31
-        const int kt = ks >> 1, qt = ks & 1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          e[kt][qt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, qt ? nm1 : nm0));
+        for (int qt = 0; qt < kPfQt; ++qt) {
+          s[2][qt] = pf_mfma(k2, qf[qt][ks], s[2][qt]);
+          s[3][qt] = pf_mfma(k3, qf[qt][ks], s[3][qt]);
+        }
+        // (kt, qt) pairs ks * kPfQt / 2 .. of keys 0..31: kt = pair / kPfQt
 #pragma unroll
-        for (int r = 0; r < 4; ++r) asm volatile("" ::"v"(e[kt][qt][r]));  // not sunk into a later block
+        for (int u = 0; u < kPfQt / 2; ++u) {
+          const int pr = ks * (kPfQt / 2) + u, kt = pr / kPfQt, qt = pr % kPfQt;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            e[kt][qt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, nm[qt]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) asm volatile("" ::"v"(e[kt][qt][r]));  // not sunk into a later block
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -292,9 +311,9 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
       mask(2);
       mask(3);
     }
-    float mloc[2];
+    float mloc[kPfQt];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < kPfQt; ++qt) {
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -304,11 +323,13 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       mloc[qt] = mx;
     }
-    const bool grow = (mloc[0] > m[0] && (m[0] == -INFINITY || (mloc[0] - m[0]) * p.scale_log2 > kLazyMax)) ||
-                      (mloc[1] > m[1] && (m[1] == -INFINITY || (mloc[1] - m[1]) * p.scale_log2 > kLazyMax));
+    bool grow = false;
+#pragma unroll
+    for (int qt = 0; qt < kPfQt; ++qt)
+      grow |= mloc[qt] > m[qt] && (m[qt] == -INFINITY || (mloc[qt] - m[qt]) * p.scale_log2 > kLazyMax);
     if (__ballot(grow) != 0) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < kPfQt; ++qt) {
         const float m_new = fmaxf(m[qt], mloc[qt]);
         const float alpha = m[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m[qt] - m_new) * p.scale_log2);
         m[qt] = m_new;
@@ -327,9 +348,11 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
                         pk_bf16(e[2 * kk + 1][qt][0], e[2 * kk + 1][qt][1]),
                         pk_bf16(e[2 * kk + 1][qt][2], e[2 * kk + 1][qt][3]));
     };
-    const uint4 p00 = pfrag(0, 0), p01 = pfrag(0, 1);
+    uint4 p0[kPfQt];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < kPfQt; ++qt) p0[qt] = pfrag(0, qt);
+#pragma unroll
+    for (int qt = 0; qt < kPfQt; ++qt) {
       const float nm = neg_m(qt);
       expo(2, qt, nm);
       expo(3, qt, nm);
@@ -339,7 +362,7 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
     // 32 kk + 16 + {4 q4 ..}) by two transposing reads: lane (s = j, g = q4)
     // addresses row 32 kk (+ 16) + 4 g + s / 4, dims 16 dt + 4 (s % 4) ..,
     // so lane j receives dim 16 dt + j of rows 32 kk (+ 16) + 4 g + e.
-    auto pv = [&](int kk, const uint4& pa, const uint4& pb) {
+    auto pv = [&](int kk, const uint4 (&pa)[kPfQt]) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         // chunk 2 dt + (j >> 1 & 1) of row x = 4 q4 + j / 4 (mod 16) sits at
@@ -348,14 +371,19 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
         const uint2 lo = lds_tr16(base + 32 * kk * kKRow);
         const uint2 hi = lds_tr16(base + (32 * kk + 16) * kKRow);
         const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        o[dt][0] = pf_mfma(vf, pa, o[dt][0]);
-        o[dt][1] = pf_mfma(vf, pb, o[dt][1]);
+#pragma unroll
+        for (int qt = 0; qt < kPfQt; ++qt) o[dt][qt] = pf_mfma(vf, pa[qt], o[dt][qt]);
       }
     };
-    pv(0, p00, p01);
-    pv(1, pfrag(1, 0), pfrag(1, 1));
+    pv(0, p0);
+    {
+      uint4 p1[kPfQt];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < kPfQt; ++qt) p1[qt] = pfrag(1, qt);
+      pv(1, p1);
+    }
+#pragma unroll
+    for (int qt = 0; qt < kPfQt; ++qt) {
       float psum = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -371,7 +399,7 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
   }
   // ---- normalise and store: lane holds dims 16 dt + 4 q4 + r of query j ----
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < kPfQt; ++qt) {
     float lt = l[qt];
     lt += __shfl_xor(lt, 16, 64);
     lt += __shfl_xor(lt, 32, 64);
