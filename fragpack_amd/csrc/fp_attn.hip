@@ -99,8 +99,6 @@ __host__ __device__ __forceinline__ int ud_offset(int units) { return (2 + 4 * u
 
 __device__ __forceinline__ int pages_of(const int32_t* seq_lens, int b) { return (seq_lens[b] + 127) >> 7; }
 
-__device__ __forceinline__ int chunks_of(int pages, int ppc) { return (pages + ppc - 1) / ppc; }
-
 // Work plan (layout of the reference planner, fused_attn_decode.cu:48-163;
 // policy of this build).  Every sequence is cut into chunks of ``ppc``
 // pages.  The reference takes the smallest ``ppc`` whose chunks fit one wave
@@ -797,7 +795,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
       decode_slab<true>(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0], sh.qt, n, c,
-                  [&](auto a, const uint4& w0, const uint4& w1, const uint4& qa) {
+                  [&](auto, const uint4& w0, const uint4& w1, const uint4& qa) {
                     s0 = mfma(a_frag(w0, w1, 0), qa, s0);
                     s1 = mfma(a_frag(w0, w1, 1), qa, s1);
                   });
@@ -878,7 +876,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
       decode_slab<true>(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
-                  [&](auto a, const uint4& w0, const uint4& w1, const uint4& pa) {
+                  [&](auto, const uint4& w0, const uint4& w1, const uint4& pa) {
                     o0 = mfma(a_frag(w0, w1, 0), pa, o0);
                     o1 = mfma(a_frag(w0, w1, 1), pa, o1);
                   });

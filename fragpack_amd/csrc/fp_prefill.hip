@@ -84,9 +84,6 @@ __device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, pf_bf16x2));
 }
 
-__device__ __forceinline__ uint32_t pf_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi, lo, sel);
-}
 
 typedef __amdgpu_buffer_rsrc_t pf_rsrc_t;
 typedef __attribute__((address_space(3))) void* pf_lds_ptr_t;

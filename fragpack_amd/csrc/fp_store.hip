@@ -504,14 +504,6 @@ __device__ __forceinline__ void stage_record(EncStage& st_buf, const uint8_t* sr
                                      0);
 }
 
-// Record r of the step: block close_list[r % n_closes], record r / n_closes
-// of it -- consecutive records (running at the same time) belong to
-// different blocks, so their fill-counter CAS rarely collide.
-__device__ __forceinline__ const uint8_t* record_src(const Store& s, int layer, int r, int n_closes) {
-  const int b = s.close_list[r % n_closes];
-  return staging_addr(s, s.wslot[b], layer, r / n_closes);
-}
-
 #ifdef FP_TRACE_ENC
 // Optional per-workgroup phase sums (built only with -DFP_TRACE_ENC): slot k
 // accumulates s_memrealtime (100 MHz) at trace point k in registers over the
