@@ -132,14 +132,17 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
     for _ in range(2):
         step_ms = timed(step)
         kern_ms = timed(lambda: step(False))
-    # the same step captured once and replayed as a HIP graph
+    # the same step captured 16 times into one HIP graph (as a serving
+    # engine captures a decode step of many layers) and replayed; per step
+    graph_steps = 16
     side = torch.cuda.Stream()
     side.wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        step(True)
+        for _ in range(graph_steps):
+            step(True)
     graph.replay()
-    graph_ms = timed(graph.replay)
+    graph_ms = timed(graph.replay) / graph_steps
     comp_ratio = rec_bytes / (2 * used.size * H * 32768)
     log(f"step {step_ms * 1e3:.1f} us, attn kernel {kern_ms * 1e3:.1f} us, "
         f"compressed {rec_bytes / 1e6:.1f} MB ({comp_ratio:.3f} of raw), effective BF16 {eff_bytes / 1e6:.1f} MB")
