@@ -528,9 +528,24 @@ __device__ uint64_t fp_enc_trace[1024 * 16];
 // every run (the reference's encode claims page space in arrival order, so
 // which record spills can change from run to run; its import places by a
 // prefix over the lengths, hbm_kv.cu:628-642).
-template <bool kBlockMajor>
+//
+// The same placement in two parallel passes, for steps that close too few
+// blocks to fill the device block by block: kMeasure analyses every record
+// (no stores) and leaves in its table entries the variable length it codes
+// to (rec_len; the raw length if it does not code) and the block's page fill
+// (rec_addr); kPlaced then encodes every record in parallel, thread 0 of
+// each workgroup walking the block's earlier records' lengths to find its
+// offset by the rule above.  An earlier record of the same block may already
+// have been finished by kPlaced: its entry then holds its final length --
+// the same variable length if it was placed, the raw length if it spilled
+// -- and either value leads to the same walk.  The block's last record
+// writes the page fill.
+enum EncMode { kEncClaim = 0, kEncBlockMajor = 1, kEncMeasure = 2, kEncPlaced = 3 };
+
+template <int kMode>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kEncodeWgPerCu)))
 encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint8_t* rank_of) {
+  constexpr bool kBlockMajor = kMode == kEncBlockMajor;
   __shared__ EncShared sh;
   __shared__ EncStage stage;
   const int tid = threadIdx.x;
@@ -586,11 +601,16 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       sh.tb[tid] = table_byte(rank_of[((int64_t)layer * per + kvh) * 256 + tid]);
       rank_kvh = kvh;
     }
-    for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
+    if (kMode != kEncMeasure)
+      for (int i = tid; i < kVarCap / 4; i += kThreads) sh.var32[i] = 0;
     // the fill value is only a first guess for the claim: fetch it early
     int cur = 0;
     if (kBlockMajor) {
       if (tid == 0 && kvh == 0) boff = *fill;  // only this workgroup places this block's records
+    } else if (kMode == kEncMeasure) {
+      if (tid == 0) cur = *fill;  // no pass writes it before kPlaced's last record
+    } else if (kMode == kEncPlaced) {
+      if (tid == 0) cur = (int)s.rec_addr[idx];  // the fill kMeasure left here
     } else if (tid == 0) {
       cur = __hip_atomic_load(fill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -619,7 +639,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       cw = nw;
       load_meta(k + 65, nb, nh, nw);
     }
-    if (heir >= 0) {
+    if (kMode != kEncMeasure && heir >= 0) {
       const uint8_t* from = staging_addr(s, s.wslot[heir], layer, kvh);
 #pragma unroll
       for (int st = 0; st < 8; ++st)
@@ -632,7 +652,34 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     int eo, ro;
     const EncResult res = enc_analyse(wd, sh, sym, code, nib, eo, ro);
     ENC_STAMP(3);
-    if (kBlockMajor && res.codes) {
+    if (kMode == kEncMeasure) {
+      if (tid == 0) {
+        s.rec_len[idx] = res.codes ? res.var_len : kRawVarLen;
+        s.rec_addr[idx] = cur;
+      }
+      lds_barrier();  // sh (wsum; rank on a head change) is reused by the next record
+      b = b1;
+      heir = heir1;
+      src = src1;
+      continue;
+    }
+    if (kMode == kEncPlaced) {
+      if (tid == 0) {
+        // the block's earlier records in (kv, head) order
+        const int32_t* lens = s.rec_len + ((int64_t)layer * s.NB + b) * per;
+        int off = cur;
+        for (int q = 0; q < kvh; ++q) {
+          const int l = lens[q];
+          if (l <= kVarCap && off + kDenseBytes + l <= page_bytes) off += kDenseBytes + l;
+        }
+        const int need = kDenseBytes + res.var_len;
+        const bool fits = res.codes && off + need <= page_bytes;
+        sh.s_off = fits ? off : -1;
+        n_spill += res.codes && !fits;
+        if (kvh == per - 1) *fill = fits ? off + need : off;  // the block's records are placed
+      }
+      if (res.codes) enc_var(wd, code, nib, sh, res, eo, ro);
+    } else if (kBlockMajor && res.codes) {
       const int need = kDenseBytes + res.var_len;
       enc_var(wd, code, nib, sh, res, eo, ro);
       ENC_STAMP(4);
@@ -1110,14 +1157,23 @@ static int encode_launch(const fp_store_t* d, const uint8_t* rank_of, int64_t ra
     cus = n;
   }
   const int64_t records = max_close * 2 * d->kv_heads;
-  if (ordered) {
-    const int64_t grid = std::min<int64_t>(max_close, (int64_t)cus * kEncodeWgPerCu);
-    hipLaunchKernelGGL(encode_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
-                       reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+  const int64_t slots = (int64_t)cus * kEncodeWgPerCu;
+  const int64_t grid = std::min<int64_t>(records, slots);
+  uint8_t* arena_p = reinterpret_cast<uint8_t*>(arena);
+  if (!ordered) {
+    hipLaunchKernelGGL(encode_kernel<kEncClaim>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
+                       arena_p, page_bytes, rank_of);
+  } else if (2 * ((records + slots - 1) / slots) < 2 * d->kv_heads) {
+    // few blocks: two parallel passes (each record read twice) finish
+    // before one workgroup per block has walked its 2H records
+    hipLaunchKernelGGL(encode_kernel<kEncMeasure>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
+                       arena_p, page_bytes, rank_of);
+    FP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(encode_kernel<kEncPlaced>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
+                       arena_p, page_bytes, rank_of);
   } else {
-    const int64_t grid = std::min<int64_t>(records, (int64_t)cus * kEncodeWgPerCu);
-    hipLaunchKernelGGL(encode_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
-                       reinterpret_cast<uint8_t*>(arena), page_bytes, rank_of);
+    hipLaunchKernelGGL(encode_kernel<kEncBlockMajor>, dim3((unsigned)std::min<int64_t>(max_close, slots)),
+                       dim3(kThreads), 0, stream, s, (int)layer, arena_p, page_bytes, rank_of);
   }
   FP_LAUNCH_CHECK();
   return 0;

@@ -124,12 +124,14 @@ int fp_hbm_write(const fp_store_t* s, const void* key, int64_t k_s0, int64_t k_s
 int fp_hbm_encode(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
                   int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream);
 
-/* fp_hbm_encode with placement by record order (SURVEY next item
- * "deterministic page packing"; no counterpart in the reference, whose
- * encode claims page space in arrival order, hbm_kv.cu:352-363): each closed
- * block's 2H records are placed in (kv, head) order, a coded record taking
- * the page's next bytes if they fit and spilling to the overflow pool if
- * not, so the arena bytes and the spill set depend only on the records. */
+/* fp_hbm_encode with placement by record order (deterministic page packing;
+ * no counterpart in the reference, whose encode claims page space in arrival
+ * order, hbm_kv.cu:352-363): each closed block's 2H records are placed in
+ * (kv, head) order, a coded record taking the page's next bytes if they fit
+ * and spilling to the overflow pool if not, so the arena bytes and the spill
+ * set depend only on the records.  For few closing blocks this runs two
+ * launches and uses the closing records' rec_addr / rec_len entries between
+ * them: nothing may read those entries before the call's work completes. */
 int fp_hbm_encode_ordered(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
                           int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream);
 

@@ -1,5 +1,9 @@
 """Ordered encode (fp_hbm_encode_ordered) on the GPU vs the placement rule.
 
+Both of its paths are covered: a step closing few blocks (two parallel
+passes: measure, then place) and one closing enough blocks to fill the
+device block by block (one workgroup walks each block's records).
+
 The rule: each closed block's 2H records, in (kv, head) order, are coded
 (the oracle's encode_record); a record that codes takes the block page's
 next bytes if they fit, else it spills raw to the overflow pool; a record
@@ -21,11 +25,11 @@ from tests.conftest import gpu_available
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 
-H, D, T, NB = 4, 128, 128, 24
+H, D, T = 4, 128, 128
 DENSE, RAW = 22528, 32768
 
 
-def _case(seed):
+def _case(seed, NB):
     from oracle import oracle
 
     rng = np.random.default_rng(seed)
@@ -41,6 +45,7 @@ def _case(seed):
 
 
 def _expected(table, kv, page):
+    NB = kv.shape[0]
     """Per (block, kv, head): page offset, or -1 for the pool; plus counts."""
     from oracle import oracle
 
@@ -64,6 +69,7 @@ def _expected(table, kv, page):
 
 
 def _run(table, kv, page):
+    NB = kv.shape[0]
     import torch
 
     from fragpack_amd.compression.attn_tables import device_tables
@@ -92,12 +98,14 @@ def _run(table, kv, page):
                                         ("spills", hbm_kv._SPILLS), ("err_overflow", hbm_kv._ERR_OVERFLOW))}, got)
 
 
-@pytest.mark.parametrize("seed", [1, 2])
-def test_ordered_encode_places_by_record_order(seed):
-    table, kv = _case(seed)
+# 24 blocks take the two-pass path, 400 the block-major one (2 x ceil(400 x 8
+# records / 1024 workgroup slots) >= 8 records per block)
+@pytest.mark.parametrize("seed,NB", [(1, 24), (2, 24), (3, 400)])
+def test_ordered_encode_places_by_record_order(seed, NB):
+    table, kv = _case(seed, NB)
     page = 2 * H * DENSE + 3 * 1280
     where, recs, spills, fallbacks = _expected(table, kv, page)
-    print("ordered encode", seed, "spills", spills, "fallbacks", fallbacks, flush=True)
+    print("ordered encode", seed, NB, "spills", spills, "fallbacks", fallbacks, flush=True)
     assert spills > 0  # the case must exercise the order
     runs = [_run(table, kv, page) for _ in range(2)]
     for addr, length, arena, abase, obase, osize, counters, got in runs:
