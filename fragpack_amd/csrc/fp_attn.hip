@@ -814,8 +814,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       float mloc = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      mloc = xor32_max(xor16_max(mloc));
       if (lane < 8) sh.red[w][lane] = mloc;
       // Softmax against the running max m_run, speculatively: the page max is
       // known only after the barrier.  P = exp2((s - m_run) c) stays exact
@@ -891,8 +890,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
     // ---- this unit's result: O of the wave's 32 dims, m, and l summed over waves ----
     float l_tot = l_run;
-    l_tot += __shfl_xor(l_tot, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
+    l_tot = xor32_sum(xor16_sum(l_tot));
     __syncthreads();  // everyone is past B2's reads of red
     if (lane < 8) sh.red[w][lane] = l_tot;
     __syncthreads();

@@ -85,6 +85,26 @@ __device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
 }
 
 
+// Butterfly partners across 16- and 32-lane halves with the gfx950 lane
+// swaps (VALU, no LDS round trip): with both operands x, one result holds
+// the lane's own value and the other its partner's (lane ^ 16 / lane ^ 32).
+__device__ __forceinline__ float pf_xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pf_xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pf_xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pf_xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 typedef __amdgpu_buffer_rsrc_t pf_rsrc_t;
 typedef __attribute__((address_space(3))) void* pf_lds_ptr_t;
 
@@ -316,8 +336,7 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = pf_xor32_max(pf_xor16_max(mx));
       mloc[qt] = mx;
     }
     bool grow = false;
@@ -398,8 +417,7 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
   for (int qt = 0; qt < kPfQt; ++qt) {
     float lt = l[qt];
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+    lt = pf_xor32_sum(pf_xor16_sum(lt));
     if (!rvalid[qt]) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     uint16_t* orow = p.out + (int64_t)(q0 + tok[qt]) * p.out_stride + (int64_t)hq[qt] * kPfDim;

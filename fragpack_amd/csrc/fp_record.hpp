@@ -378,6 +378,30 @@ __device__ __forceinline__ void raw_words(const SlabBuf& b, rsrc_t r, int slab, 
   emit(std::integral_constant<int, 7>{}, w7);
 }
 
+// Butterfly partner values across 16- and 32-lane halves with the gfx950
+// lane-swap instructions (VALU, no LDS round trip): v_permlane16_swap swaps
+// the odd 16-lane rows of its first operand with the even rows of its
+// second, v_permlane32_swap the upper half of the first with the lower half
+// of the second; with both operands x, each lane ends up holding its own
+// value in one result and its partner's (lane ^ 16, lane ^ 32) in the other,
+// so a symmetric op of the two results is the butterfly step.
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Table words of one (kv, head): primary bytes and the 16-byte extended table.
 struct HeadLut {
   uint32_t p0, p1;
