@@ -465,6 +465,7 @@ struct AttnShared {
   uint8_t pt[kTileBytes];      // P tile
   uint8_t qt[kTileBytes];      // Q tile, even-odd slot order
   float red[kWaves][8];        // per-wave page max / final l per head
+  int plan[kWaves][4][64];     // inline plan per wave: first unit, chunks, context, pages by sequence
   int last;
 };
 
@@ -640,6 +641,15 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   InlinePlan ip{0, 0, 0, 0, 1, 0};
   if constexpr (kInlinePlan) ip = inline_plan(p, lane);
   const int used = kInlinePlan ? ip.used : uniform(p.plan[1]);  // units in use
+  const int ppc = ip.ppc;
+  if constexpr (kInlinePlan) {
+    // the per-sequence plan goes to this wave's LDS rows (read back by
+    // sequence), so its four registers are free during the page loop
+    sh.plan[w][0][lane] = ip.first;
+    sh.plan[w][1][lane] = ip.cnt;
+    sh.plan[w][2][lane] = ip.len;
+    sh.plan[w][3][lane] = ip.n;
+  }
   if (kInlinePlan && blockIdx.x == 0 && h == 0 && w == 0) {
     // the plan words for later calls that reuse this plan
     int32_t* plan = p.plan;
@@ -665,13 +675,13 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     int b, p0, npages, seq, first, chunks, blk0;
     if constexpr (kInlinePlan) {
       // the last live sequence whose first unit is <= unit owns it
-      const uint64_t own = __ballot(lane < p.batch && ip.cnt > 0 && ip.first <= unit);
+      const uint64_t own = __ballot(lane < p.batch && sh.plan[w][1][lane] > 0 && sh.plan[w][0][lane] <= unit);
       b = 63 - __builtin_clzll(own);
-      first = __builtin_amdgcn_readlane(ip.first, b);
-      chunks = __builtin_amdgcn_readlane(ip.cnt, b);
-      seq = __builtin_amdgcn_readlane(ip.len, b);
-      p0 = (unit - first) * ip.ppc;
-      npages = min(__builtin_amdgcn_readlane(ip.n, b), p0 + ip.ppc) - p0;
+      first = uniform(sh.plan[w][0][b]);
+      chunks = uniform(sh.plan[w][1][b]);
+      seq = uniform(sh.plan[w][2][b]);
+      p0 = (unit - first) * ppc;
+      npages = min(uniform(sh.plan[w][3][b]), p0 + ppc) - p0;
       blk0 = uniform(p.block_table[(int64_t)b * p.bt_stride + p0]);
       if (h == 0 && threadIdx.x == 0) {
         // this unit's plan entries for later calls
@@ -922,7 +932,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
     for (int b = w; b < p.batch; b += kWaves) {
-      const int cnt = kInlinePlan ? __builtin_amdgcn_readlane(ip.cnt, b) : p.plan[3 + 2 * p.units + 2 * b];
+      const int cnt = kInlinePlan ? sh.plan[w][1][b] : p.plan[3 + 2 * p.units + 2 * b];
       if (cnt != 0) continue;
       uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)h * p.group * kDim);
       for (int x = lane; x < p.group * kDim / 2; x += 64) orow[x] = 0u;
