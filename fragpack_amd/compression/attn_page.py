@@ -14,9 +14,15 @@ record whose variable region exceeds ``VAR_CAP`` or with more than
 ``MAX_WARP_RAW`` raw scalars in a 2048-scalar slab is stored raw
 (``RAW_RECORD_BYTES``).  The byte format is the reference's, unchanged.
 
-``encode_record`` / ``decode_record`` run on the GPU (the batch codec
-kernels of libfragpack_hip.so); there is no CPU codec in this package.
-Table calibration and LUT packing are host-side numpy, as in the reference.
+``encode_record`` / ``decode_record`` are the host codec (numpy, no GPU
+needed, as the reference's are): every byte of a record is placed through
+index maps computed once per kv from the kernel order -- which token-major
+scalar each dense low byte holds, which scalars feed each nibble of each
+symbol word, which scalar each raw-form halfword holds -- so encode and
+decode are gathers and scatters over those maps.  ``encode_records`` /
+``decode_records`` are the GPU batch codec (libfragpack_hip.so kernels),
+byte-identical to the host codec.  Table calibration and LUT packing are
+host-side numpy, as in the reference.
 """
 
 from __future__ import annotations
@@ -90,11 +96,168 @@ def rank_of(table: NDArray[np.uint8]) -> NDArray[np.uint8]:
     return r
 
 
+# ---------------------------------------------------------------------------
+# Host codec.  Byte placement of a coded record (attn_page.py:56-80 format):
+#   low byte of kernel-order scalar 64 t + 16 j + i  -> byte 16 (256 j + t) + i
+#   symbol word (group G = 2 t + gi, k)              -> u32 at LOW_BYTES +
+#       8 (256 m + t) + 4 x with 2 m + x = 3 gi + k; nibble n of that word is
+#       (code of scalar 32 G + 8 k + n) & 7 | (bit k of code 32 G + 24 + n) << 3
+#   raw form: kernel-order scalar 64 t + 8 st + i    -> u16 at 16 (256 st + t) + 2 i
+# The maps below give, for each output position, the token-major scalar it
+# reads (composed with the kernel order of K or V).
+
+_SYM_WORDS = SYMBOL_BYTES // 4  # 1536 u32 words: 3 per 32-scalar group
+
+
+def _placement_maps(kv: int) -> dict[str, NDArray[np.int64]]:
+    order = kernel_order(kv)  # kernel-order position -> token-major scalar
+    pos = np.arange(LOW_BYTES)
+    j, t, i = pos >> 12, (pos >> 4) & 255, pos & 15
+    low = order[64 * t + 16 * j + i]
+    q = np.arange(_SYM_WORDS)
+    m, t, x = q // 512, (q >> 1) & 255, q & 1
+    gk = 2 * m + x  # 3 gi + k
+    group = 2 * t + gk // 3
+    k = gk % 3
+    n = np.arange(8)
+    code_src = order[32 * group[:, None] + 8 * k[:, None] + n[None, :]]  # [word, nibble]: 3 code bits
+    bit_src = order[32 * group[:, None] + 24 + n[None, :]]              # [word, nibble]: one bit of this code
+    h = np.arange(RECORD_SCALARS)
+    st, t, i = h >> 11, (h >> 3) & 255, h & 7
+    raw = order[64 * t + 8 * st + i]
+    return {"order": order, "low": low, "code_src": code_src, "bit_src": bit_src, "bit_k": k, "raw": raw}
+
+
+_MAPS = (_placement_maps(0), _placement_maps(1))
+_NIB_SHIFT = (4 * np.arange(8)).astype(np.uint32)
+_HEADER = struct.Struct("<4I8H8H")
+
+
+def _checked_kv(kv: int) -> int:
+    if kv not in (0, 1):
+        raise ValueError(f"kv must be 0 (K) or 1 (V), got {kv}")
+    return int(kv)
+
+
+def encode_record(raw: NDArray[np.uint16], table: NDArray[np.uint8], kv: int) -> bytes:
+    """Encode one token-major ``[128, 128]`` BF16 record on the host
+    (attn_page.py:146-209).
+
+    Args:
+        raw: BF16 bit patterns as uint16 (``PAGE_TOKENS * HEAD_DIM`` of them).
+        table: The head's 22-entry table (:func:`calibrate_table`).
+        kv: 0 for a K record, 1 for a V record (selects the kernel order).
+
+    Returns:
+        The record (16-byte aligned length), coded, or the ``RAW_RECORD_BYTES``
+        raw form when the variable region would exceed ``VAR_CAP`` or a
+        2048-scalar slab would hold more than ``MAX_WARP_RAW`` raw scalars.
+
+    Raises:
+        ValueError: If ``raw`` has the wrong size or ``kv`` is not 0 / 1.
+
+    Async/thread-safety:
+        Pure function.
+    """
+    tm = np.ascontiguousarray(raw, dtype=np.uint16).reshape(-1)
+    if tm.size != RECORD_SCALARS:
+        raise ValueError("record must hold PAGE_TOKENS * HEAD_DIM scalars")
+    mp = _MAPS[_checked_kv(kv)]
+    ranks = rank_of(table)[tm >> 8]  # per token-major scalar
+    seq = ranks[mp["order"]]         # in kernel order
+    esc = seq >= PRIMARY_DIRECT
+    is_raw = seq >= TABLE_ENTRIES
+    slab_raw = is_raw.reshape(WARPS, WARP_SCALARS).sum(axis=1)
+    esc_ranks = seq[esc]
+    n_esc, n_raw = int(esc_ranks.size), int(slab_raw.sum())
+    raw_offset = (HEADER_BYTES + (n_esc + 1) // 2 + 3) & ~3
+    var_len = (raw_offset + 4 * n_raw + 15) & ~15
+    if var_len > VAR_CAP or int(slab_raw.max()) > MAX_WARP_RAW:
+        return tm[mp["raw"]].astype("<u2").tobytes()
+    out = np.zeros(DENSE_BYTES + var_len, np.uint8)
+    out[:LOW_BYTES] = tm[mp["low"]] & 0xFF
+    code = np.minimum(ranks, PRIMARY_DIRECT).astype(np.uint32)
+    nib = (code[mp["code_src"]] & 7) | (((code[mp["bit_src"]] >> mp["bit_k"][:, None]) & 1) << 3)
+    out[LOW_BYTES:DENSE_BYTES] = (nib << _NIB_SHIFT).sum(axis=1, dtype=np.uint32).astype("<u4").view(np.uint8)
+    # variable region: header, escape nibbles (low nibble first), raw list
+    slab_esc = esc.reshape(WARPS, WARP_SCALARS).sum(axis=1)
+    esc_prefix = np.cumsum(slab_esc) - slab_esc
+    raw_prefix = np.cumsum(slab_raw) - slab_raw
+    var = out[DENSE_BYTES:]
+    var[:HEADER_BYTES] = np.frombuffer(_HEADER.pack(n_esc, n_raw, raw_offset, 0, *esc_prefix, *raw_prefix), np.uint8)
+    nibbles = np.where(esc_ranks < TABLE_ENTRIES, esc_ranks.astype(np.int32) - PRIMARY_DIRECT, RAW_NIBBLE)
+    packed = np.zeros((n_esc + 1) // 2 * 2, np.uint8)
+    packed[:n_esc] = nibbles
+    var[HEADER_BYTES : HEADER_BYTES + packed.size // 2] = packed[0::2] | (packed[1::2] << 4)
+    ordinals = np.flatnonzero(esc_ranks >= TABLE_ENTRIES).astype(np.uint32)
+    highs = (tm[mp["order"]][is_raw] >> 8).astype(np.uint32)
+    var[raw_offset : raw_offset + 4 * n_raw] = (ordinals | (highs << 16)).astype("<u4").view(np.uint8)
+    return out.tobytes()
+
+
+def decode_record(record: bytes, table: NDArray[np.uint8], kv: int) -> NDArray[np.uint16]:
+    """Decode one record (coded or raw) on the host (attn_page.py:212-269).
+
+    Args:
+        record: Bytes from :func:`encode_record` (or the arena / overflow).
+        table: The table it was coded with.
+        kv: The ``kv`` it was coded with.
+
+    Returns:
+        uint16 ``[128, 128]`` token-major BF16 bit patterns.
+
+    Raises:
+        ValueError: If the length is impossible or the variable region is
+            inconsistent with the symbols.
+
+    Async/thread-safety:
+        Pure function.
+    """
+    mp = _MAPS[_checked_kv(kv)]
+    buf = np.frombuffer(record, np.uint8)
+    out = np.empty(RECORD_SCALARS, np.uint16)
+    if buf.size == RAW_RECORD_BYTES:
+        out[mp["raw"]] = buf.view("<u2")
+        return out.reshape(PAGE_TOKENS, HEAD_DIM)
+    if not DENSE_BYTES + HEADER_BYTES <= buf.size <= DENSE_BYTES + VAR_CAP:
+        raise ValueError(f"record length {buf.size} is neither raw nor coded")
+    tab = np.asarray(table, np.uint8)
+    words = buf[LOW_BYTES:DENSE_BYTES].view("<u4").astype(np.uint32)
+    nib = (words[:, None] >> _NIB_SHIFT) & 15  # [word, nibble]
+    code = np.zeros(RECORD_SCALARS, np.uint32)  # token-major
+    code[mp["code_src"]] = nib & 7
+    np.bitwise_or.at(code, mp["bit_src"], (nib >> 3) << mp["bit_k"][:, None].astype(np.uint32))
+    var = buf[DENSE_BYTES:]
+    n_esc, n_raw, raw_offset = _HEADER.unpack_from(var)[:3]
+    if HEADER_BYTES + (n_esc + 1) // 2 > var.size or raw_offset + 4 * n_raw > var.size:
+        raise ValueError("variable region overruns the record")
+    seq_code = code[mp["order"]]
+    escaped = seq_code == PRIMARY_DIRECT
+    if int(escaped.sum()) != n_esc:
+        raise ValueError("escape count does not match the symbols")
+    packed = var[HEADER_BYTES : HEADER_BYTES + (n_esc + 1) // 2]
+    nibbles = np.stack([packed & 15, packed >> 4], axis=1).reshape(-1)[:n_esc]
+    highs = np.zeros(n_esc, np.uint16)
+    ext = nibbles < RAW_NIBBLE
+    highs[ext] = tab[PRIMARY_DIRECT + nibbles[ext]]
+    entries = var[raw_offset : raw_offset + 4 * n_raw].view("<u4")
+    ords = entries & 0xFFFF
+    if np.any(ords >= n_esc):
+        raise ValueError("raw entry names no escape")
+    highs[ords] = entries >> 16
+    high_seq = np.zeros(RECORD_SCALARS, np.uint16)
+    high_seq[~escaped] = tab[seq_code[~escaped]]
+    high_seq[escaped] = highs
+    out[mp["low"]] = buf[:LOW_BYTES]
+    out[mp["order"]] |= high_seq << 8
+    return out.reshape(PAGE_TOKENS, HEAD_DIM)
+
+
 def _device():
     import torch
 
     if not torch.cuda.is_available():
-        raise RuntimeError("the FragPack record codec runs on the GPU; no GPU is available")
+        raise RuntimeError("the GPU batch codec needs a GPU; encode_record / decode_record run on the host")
     return torch.device("cuda", torch.cuda.current_device())
 
 
@@ -135,24 +298,6 @@ def encode_records(raw: NDArray[np.uint16], tables: NDArray[np.uint8], kv: NDArr
     return [host[i, : ln[i]].tobytes() for i in range(n)]
 
 
-def encode_record(raw: NDArray[np.uint16], table: NDArray[np.uint8], kv: int) -> bytes:
-    """Encode one token-major ``[128, 128]`` BF16 record (attn_page.py:146-209).
-
-    Returns:
-        The record (16-byte aligned length), coded, or the ``RAW_RECORD_BYTES``
-        raw fallback.
-
-    Raises:
-        ValueError: If ``raw`` has the wrong size.
-        RuntimeError: If no GPU (or the library) is available.
-    """
-    values = np.ascontiguousarray(raw, dtype=np.uint16).reshape(-1)
-    if values.size != RECORD_SCALARS:
-        raise ValueError("record must hold PAGE_TOKENS * HEAD_DIM scalars")
-    return encode_records(values.reshape(1, PAGE_TOKENS, HEAD_DIM), np.asarray(table, np.uint8)[None],
-                          np.array([kv], np.int32), np.zeros(1, np.int32))[0]
-
-
 def decode_records(records: list[bytes], tables: NDArray[np.uint8], kv: NDArray[np.int32],
                    tab_idx: NDArray[np.int32]) -> NDArray[np.uint16]:
     """Decode many records on the GPU into uint16 ``[n, 128, 128]``."""
@@ -185,12 +330,6 @@ def decode_records(records: list[bytes], tables: NDArray[np.uint8], kv: NDArray[
         out,
     )
     return out.cpu().numpy().view(np.uint16)
-
-
-def decode_record(record: bytes, table: NDArray[np.uint8], kv: int) -> NDArray[np.uint16]:
-    """Decode one record (attn_page.py:212-269) into uint16 ``[128, 128]``."""
-    return decode_records([record], np.asarray(table, np.uint8)[None], np.array([kv], np.int32),
-                          np.zeros(1, np.int32))[0]
 
 
 def blob_head_bytes(num_layers: int, kv_heads: int) -> int:

@@ -44,14 +44,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 
-#ifndef FP_PERSIST
-#define FP_PERSIST 1
-#endif
-#ifndef FP_ATTN_WAVES_PER_EU
-#define FP_ATTN_WAVES_PER_EU 3  // occupancy target of attn_kernel (VGPR budget 512 / 3)
-#endif
-constexpr int kWaves = 4;          // wavefronts per workgroup = slabs per record
-constexpr int kAttnPerCu = FP_ATTN_WAVES_PER_EU;  // resident workgroups per CU (kWaves = SIMDs per CU)
+constexpr int kWaves = 4;     // wavefronts per workgroup = slabs per record
+constexpr int kAttnPerCu = 3;  // resident workgroups per CU (kWaves = SIMDs per CU; VGPR budget 512 / 3)
 constexpr float kLazyMax = 8.f;    // log2 headroom of the speculative softmax reference
 constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
 
@@ -443,22 +437,6 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
   decode_words<true>(b, esc, e0 + excl, lut.p0, lut.p1, emit);
 }
 
-// Optional per-workgroup timeline (built only with -DFP_TRACE): slot k of
-// workgroup (x, y) holds s_memrealtime (100 MHz) at trace point k.
-#ifdef FP_TRACE
-constexpr int kTraceSlots = 32;
-__device__ uint64_t fp_trace_buf[4096 * kTraceSlots];
-#define FP_STAMP(k)                                                                                 \
-  do {                                                                                              \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096 && (k) < kTraceSlots)              \
-      fp_trace_buf[blockIdx.x * kTraceSlots + (k)] = __builtin_amdgcn_s_memrealtime();                \
-  } while (0)
-#else
-#define FP_STAMP(k) \
-  do {              \
-  } while (0)
-#endif
-
 struct AttnShared {
   uint8_t esc[2][2][kEscLds];  // [page parity][K, V] expanded escape bytes
   uint32_t hdr[2][2][12];      // [page parity][K, V] record headers
@@ -624,7 +602,7 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
 }
 
 template <bool kInlinePlan, bool kAppend>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FP_ATTN_WAVES_PER_EU))) attn_kernel(AttnParams p) {
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kAttnPerCu))) attn_kernel(AttnParams p) {
   __shared__ AttnShared sh;
   const int lane = wave_lane();
   const int w = uniform((int)(threadIdx.x >> 6));  // this wave's slab of every record (wave-uniform)
@@ -636,7 +614,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const HeadLut klut = load_lut(p.plut, p.slut, h);
   const HeadLut vlut = load_lut(p.plut, p.slut, p.kvh + h);
 
-  FP_STAMP(0);
   // the work plan: planned here (inline) or read from the plan workspace
   InlinePlan ip{0, 0, 0, 0, 1, 0};
   if constexpr (kInlinePlan) ip = inline_plan(p, lane);
@@ -649,6 +626,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     sh.plan[w][1][lane] = ip.cnt;
     sh.plan[w][2][lane] = ip.len;
     sh.plan[w][3][lane] = ip.n;
+    // lanes read each other's rows below: order the stores before those
+    // reads for the compiler too (the wave's LDS accesses are in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   if (kInlinePlan && blockIdx.x == 0 && h == 0 && w == 0) {
     // the plan words for later calls that reuse this plan
@@ -740,7 +722,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     PageMeta meta = load_meta(p, blk, h);
 
     __syncthreads();  // the previous unit is done with every tile
-    FP_STAMP(1);
     // Q into the fragment tile: u32 pair j of row r (dims 2j, 2j + 1 =
     // 32a + 16x + 8f + 2c + e, e = 0, 1) belongs to fragment (r, a, c) at
     // slot 4x + 2e + f (even-odd order; raw K records permute the fragments
@@ -765,7 +746,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     float m_run = -INFINITY, l_run = 0.f;  // m_run: unscaled score units
     const float lazy = kLazyMax / p.scale_log2;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-    FP_STAMP(2);
     expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
     expand_var(vr, vv, w, lane, vlut.s, sh.esc[0][1], sh.hdr[0][1]);
     // page 1's variable regions: each page's are in flight a page before
@@ -800,7 +780,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         vv2 = prefetch_var(nnvr, w, lane);
       }
       __syncthreads();  // B1: this page's escapes patched; the previous page's V pass done everywhere
-      FP_STAMP(3 + 5 * min(i, 4));
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -855,14 +834,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         }
       };
       if (spec) softmax_tile(m_run);
-      FP_STAMP(4 + 5 * min(i, 4));
       if (more) {
         prefetch_dense(nkr, w, nt, fk);
         expand_var(nkr, vk, w, lane, klut.s, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
         expand_var(nvr, vv, w, lane, vlut.s, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
       }
       __syncthreads();  // B2: page max per wave known; P tile written; next page's escapes expanded
-      FP_STAMP(5 + 5 * min(i, 4));
       const float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
       // the same decision in every wave: all read the same page maxima
       if (!spec || __ballot(mpage > m_run + lazy) != 0) {
@@ -881,7 +858,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         patch_raw(nkr, vk, w, lane, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
         patch_raw(nvr, vv, w, lane, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
       }
-      FP_STAMP(6 + 5 * min(i, 4));
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
       decode_slab<true>(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
@@ -895,7 +871,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       nvr = nnvr;
       vk = vk2;
       vv = vv2;
-      FP_STAMP(7 + 5 * min(i, 4));
     }
 
     // ---- this unit's result: O of the wave's 32 dims, m, and l summed over waves ----
@@ -925,9 +900,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       st_coh4(ro, i0 + 8, o1[0], o1[1], o1[2], o1[3]);
       if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run * p.scale_log2, l_all);
     }
-    FP_STAMP(28);
     merge_chunks(p, sh, b, h, first, chunks);
-    FP_STAMP(29);
   }
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
@@ -959,11 +932,6 @@ static int decode_slots() {
   return cache[dev];
 }
 
-#ifdef FP_TRACE
-extern "C" int fp_trace_read(uint64_t* host, int64_t n) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(fp_trace_buf), n * sizeof(uint64_t)) == hipSuccess ? 0 : -1;
-}
-#endif
 
 namespace fp {
 namespace {
@@ -1021,11 +989,7 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   }
   // persistent grid: one resident wave of workgroups (slots over all KV
   // heads) walks the units in use
-#if FP_PERSIST
   const int64_t per_head = std::min<int64_t>(units, (slots + kv_heads - 1) / kv_heads);
-#else
-  const int64_t per_head = units;
-#endif
   const dim3 grid((unsigned)per_head, (unsigned)kv_heads), block(64 * kWaves);
   if (p.nk != nullptr) {
     if (p.inline_plan)

@@ -504,20 +504,6 @@ __device__ __forceinline__ void stage_record(EncStage& st_buf, const uint8_t* sr
                                      0);
 }
 
-#ifdef FP_TRACE_ENC
-// Optional per-workgroup phase sums (built only with -DFP_TRACE_ENC): slot k
-// accumulates s_memrealtime (100 MHz) at trace point k in registers over the
-// workgroup's records; written once at the end.
-__device__ uint64_t fp_enc_trace[1024 * 16];
-#define ENC_STAMP(k)                                        \
-  do {                                                      \
-    enc_tacc[(k)] += __builtin_amdgcn_s_memrealtime();      \
-  } while (0)
-#else
-#define ENC_STAMP(k) \
-  do {               \
-  } while (0)
-#endif
 
 // kBlockMajor (the ordered encode): workgroup g encodes whole blocks
 // close_list[g], close_list[g + grid], ..., each block's 2H records in
@@ -589,12 +575,8 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   int n_enc = 0, n_fall = 0, n_err = 0, n_spill = 0;
   bool ovf_full = false;  // this workgroup found the overflow pool full
   int boff = 0;           // ordered encode: the block's next free page byte (thread 0)
-#ifdef FP_TRACE_ENC
-  uint64_t enc_tacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#endif
   for (int k = 0; r < n_rec; r = next_rec(r), ++k) {
     const int kvh = rec_kvh(r);
-    ENC_STAMP(0);
     const int64_t idx = ((int64_t)layer * s.NB + b) * per + kvh;
     int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
     if (kvh != rank_kvh) {  // consecutive records mostly share (layer, kvh)
@@ -620,7 +602,6 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
 #pragma unroll
     for (int st = 0; st < 8; ++st) wd[st] = stage.w[st][tid];
     __builtin_amdgcn_s_waitcnt(0);  // reads done before the stage is refilled
-    ENC_STAMP(1);
     // the next record's metadata: lane (k + 1) % 64 of the current or next batch
     const int k1 = (k + 1) & 63;
     const bool nbatch = k1 == 0;
@@ -647,11 +628,9 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       if (tid == 0) s.rec_addr[((int64_t)layer * s.NB + heir) * per + kvh] = reinterpret_cast<int64_t>(src);
     }
     lds_barrier();
-    ENC_STAMP(2);
     uint32_t sym[6], code[8], nib[8];
     int eo, ro;
     const EncResult res = enc_analyse(wd, sh, sym, code, nib, eo, ro);
-    ENC_STAMP(3);
     if (kMode == kEncMeasure) {
       if (tid == 0) {
         s.rec_len[idx] = res.codes ? res.var_len : kRawVarLen;
@@ -682,7 +661,6 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     } else if (kBlockMajor && res.codes) {
       const int need = kDenseBytes + res.var_len;
       enc_var(wd, code, nib, sh, res, eo, ro);
-      ENC_STAMP(4);
       if (tid == 0) {
         const bool fits = boff + need <= page_bytes;
         sh.s_off = fits ? boff : -1;
@@ -695,7 +673,6 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       int prev = -1;
       if (tid == 0 && cur + need <= page_bytes) prev = atomicCAS(fill, cur, cur + need);
       enc_var(wd, code, nib, sh, res, eo, ro);
-      ENC_STAMP(4);
       if (tid == 0) {
         int off = -1;
         if (cur + need <= page_bytes) {
@@ -720,7 +697,6 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       sh.s_off = -1;
     }
     lds_barrier();
-    ENC_STAMP(5);
     if (sh.s_off < 0) {
       if (tid < 64) {
         // Nothing frees overflow slots while an encode runs (frees happen in
@@ -756,9 +732,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       }
     }
     if (kBlockMajor && tid == 0 && kvh == per - 1) *fill = boff;  // the block's records are placed
-    ENC_STAMP(6);
     lds_barrier();  // sh (var32, s_off, s_ovf; rank on a head change) is reused by the next record
-    ENC_STAMP(7);
     b = b1;
     heir = heir1;
     src = src1;
@@ -769,10 +743,6 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     if (n_err) atomicAdd(&s.counters[kErrOverflow], n_err);
     if (n_spill) atomicAdd(&s.counters[kSpills], n_spill);
   }
-#ifdef FP_TRACE_ENC
-  if (threadIdx.x == 0 && blockIdx.x < 1024)
-    for (int k = 0; k < 8; ++k) fp_enc_trace[blockIdx.x * 16 + k] = enc_tacc[k];
-#endif
 }
 
 // Closed blocks release their staging or pass it to their heir; the close
@@ -1130,12 +1100,6 @@ extern "C" int fp_hbm_write(const fp_store_t* d, const void* key, int64_t k_s0, 
   FP_LAUNCH_CHECK();
   return 0;
 }
-
-#ifdef FP_TRACE_ENC
-extern "C" int fp_enc_trace_read(uint64_t* host, int64_t n) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(fp_enc_trace), n * sizeof(uint64_t)) == hipSuccess ? 0 : -1;
-}
-#endif
 
 static int encode_launch(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
                          int64_t arena, int64_t page_bytes, int64_t max_close, bool ordered, fp_stream_t stream) {

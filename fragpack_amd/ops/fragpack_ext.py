@@ -180,18 +180,6 @@ class Extension:
         else:
             raise NotImplementedError("the fused append (fp_fused_decode_append) is disabled: its first GPU run "
                                       "faulted and the cause is not yet found; write with HbmKvStore.write")
-            nk, nv, slots, staging, scratch = append
-            _check(slots.dtype == torch.int64 and slots.numel() >= B and slots.is_contiguous(),
-                   "slot_mapping must be int64 [>= B]")
-            for t, name in ((nk, "new_k"), (nv, "new_v")):
-                _check(t.dtype == bf16 and t.dim() == 3 and t.shape[0] >= B and t.shape[1] == kvh and t.shape[2] == 128
-                       and t.stride(2) == 1, f"{name} must be BF16 [B, H, 128] with contiguous rows")
-            if self._fused_append(
-                *args, _dev(nk, "new_k"), nk.stride(0), nk.stride(1), _dev(nv, "new_v"), nv.stride(0), nv.stride(1),
-                _dev(slots, "slot_mapping"), _dev(staging, "staging"), staging.numel() * staging.element_size(), _dev(scratch, "scratch"),
-                scratch.numel() * scratch.element_size(), torch.cuda.current_stream().cuda_stream,
-            ):
-                raise RuntimeError(f"fp_fused_decode_append: {self._lib.fp_last_error().decode()}")
         if mode:
             plan._fp_counters_zeroed = True
 

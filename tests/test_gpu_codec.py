@@ -68,17 +68,23 @@ def test_random_kv_records_vs_oracle(outlier):
     assert np.array_equal(back, raw)
 
 
-def test_single_record_api():
+def test_gpu_batch_codec_equals_host_codec():
+    """The GPU batch codec and the package's host codec give the same bytes
+    and both decode each other's records."""
     from fragpack_amd.compression import attn_page as ap
 
     rng = np.random.default_rng(0)
     cal = kvgen.kv_bits(rng, (128, 128), 0.02)
     table = ap.calibrate_table((cal >> 8).astype(np.uint8))
-    rec = kvgen.kv_bits(rng, (128, 128), 0.02)
-    rec[3, 5] = 0x7F00 | (rec[3, 5] & 0xFF)
-    for kv in (0, 1):
-        enc = ap.encode_record(rec, table, kv)
-        assert len(enc) % 16 == 0 and len(enc) <= ap.DENSE_BYTES + ap.VAR_CAP
-        assert np.array_equal(ap.decode_record(enc, table, kv), rec)
-    with pytest.raises(ValueError):
-        ap.encode_record(np.zeros(10, np.uint16), table, 0)
+    recs = np.stack([kvgen.kv_bits(rng, (128, 128), 0.02) for _ in range(4)])
+    recs[1, 3, 5] = 0x7F00 | (recs[1, 3, 5] & 0xFF)
+    recs[3] = rng.integers(0, 1 << 16, (128, 128), dtype=np.uint16)  # falls back to raw
+    kv = np.array([0, 1, 0, 1], np.int32)
+    got = ap.encode_records(recs, table[None], kv, np.zeros(4, np.int32))
+    for i in range(4):
+        host = ap.encode_record(recs[i], table, int(kv[i]))
+        assert got[i] == host, i
+        assert np.array_equal(ap.decode_record(got[i], table, int(kv[i])), recs[i])
+    assert len(got[3]) == ap.RAW_RECORD_BYTES
+    back = ap.decode_records(got, table[None], kv, np.zeros(4, np.int32))
+    assert np.array_equal(back, recs)
