@@ -628,9 +628,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     sh.plan[w][3][lane] = ip.n;
     // lanes read each other's rows below: order the stores before those
     // reads for the compiler too (the wave's LDS accesses are in order)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();
   }
   if (kInlinePlan && blockIdx.x == 0 && h == 0 && w == 0) {
     // the plan words for later calls that reuse this plan

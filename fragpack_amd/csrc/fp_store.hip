@@ -36,7 +36,6 @@ enum : int {
 };
 enum : int { kTagLive = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
 
-constexpr int kPrepThreads = 1024;
 constexpr int kThreads = 256;
 constexpr int kEncodeWgPerCu = 4;  // resident encode workgroups per CU (LDS: 32 KB stage + 6 KB each)
 
@@ -144,96 +143,190 @@ __device__ __forceinline__ void ovf_free(const Store& s, int64_t addr) {
 }
 
 // ---------------------------------------------------------------------------
-// prepare: one workgroup, phases separated by barriers (hbm_kv.cu:110-219):
-// GC of unreferenced staging, close marks (offset 127), claims (offset 0)
-// with transient / heir slots, the close list with heirs paired to donors,
-// then claimed blocks' records pointed at their staging.
+// prepare / commit: a step's staging bookkeeping on one 1024-thread workgroup,
+// with the semantics of the reference's prepare and commit
+// (hbm_kv.cu:110-219, 431-448): GC of staging no live block holds, close
+// marks (offset 127), claims (offset 0) served from transient scratch, the
+// free stack or -- when it is empty -- transient scratch as an heir of a
+// closing block, the close list with heirs paired to donors, and the claimed
+// blocks' records pointed at their staging.
+//
+// Every list is built by workgroup stream compaction in input order: a
+// thread takes kCompactPer consecutive items per round, its count is scanned
+// across the wave with DPP and across the 16 waves through LDS, and each
+// item lands at its rank.  All counters stay in registers / LDS until one
+// store at the end -- no per-item global atomics -- and the outcome is a
+// function of the state and the step: the same step on the same state gives
+// the same slot assignment, list order and heir pairing.  Liveness is an LDS
+// bitmap over persistent slots (a live block's slot bit), so GC needs no tag
+// round trip.  The lists borrow the close list as scratch before the close
+// phase writes it: deduplicated claims at close_list[0 ..), claims past the
+// transient scratch at close_list[cap ..).
+constexpr int kPrepThreads = 1024;
+constexpr int kPrepWaves = kPrepThreads / 64;
+constexpr int kCompactPer = 4;
+constexpr int kLiveWords = 8192;  // persistent-slot liveness bitmap: up to 262144 slots
+
+struct PrepShared {
+  uint32_t live[kLiveWords];
+  int wcnt[kPrepWaves];
+};
+
+// Stream compaction of items [0, n): ``pick(i)`` returns a payload >= 0 to
+// keep item i (or < 0), ``emit(i, rank, payload)`` receives each kept item's
+// rank in input order.  Called by the whole workgroup; returns the count,
+// with every emit's stores done before it returns.
+template <typename Pick, typename Emit>
+__device__ int wg_compact(int n, PrepShared& sh, Pick pick, Emit emit) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int total = 0;
+  for (int r0 = 0; r0 < n; r0 += kCompactPer * kPrepThreads) {
+    const int i0 = r0 + kCompactPer * tid;
+    int pay[kCompactPer], cnt = 0;
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k) {
+      pay[k] = i0 + k < n ? pick(i0 + k) : -1;
+      cnt += pay[k] >= 0;
+    }
+    const int incl = wave_incl_scan(cnt);
+    if (lane == 63) sh.wcnt[wave] = incl;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kPrepWaves; ++w) {
+      const int c = sh.wcnt[w];
+      before += w < wave ? c : 0;
+      all += c;
+    }
+    __syncthreads();  // wcnt is rewritten by the next round
+    int rank = total + before + incl - cnt;
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k)
+      if (pay[k] >= 0) emit(i0 + k, rank++, pay[k]);
+    total += all;
+  }
+  __syncthreads();  // every emit is visible to the workgroup's next phase
+  return total;
+}
+
+__device__ __forceinline__ int slot_block(const Store& s, int64_t sl, int offset) {
+  return sl >= 0 && (int)(sl & 127) == offset && (sl >> 7) < s.NB ? (int)(sl >> 7) : -1;
+}
+
 __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const int64_t* slots, int n_tok,
                                                                const int32_t* live, int n_live, int32_t step) {
+  __shared__ PrepShared sh;
   const int tid = threadIdx.x;
-  int32_t* live_tag = s.tags + kTagLive * s.NB;
   int32_t* close_tag = s.tags + kTagClose * s.NB;
   int32_t* claim_tag = s.tags + kTagClaim * s.NB;
   int32_t* dedupe_tag = s.tags + kTagCloseDedupe * s.NB;
-  if (tid == 0) {
-    s.counters[kTrans] = 0;
-    s.counters[kClaims] = 0;
-    s.counters[kCloses] = 0;
-    s.counters[kHeirs] = 0;
-    s.counters[kDonors] = 0;
-  }
-  for (int i = tid; i < n_live; i += kPrepThreads) live_tag[live[i]] = step;
+  int32_t* tmp = s.close_list;             // deduplicated claims (scratch until the close phase)
+  int32_t* late = s.close_list + s.cap;    // closing claims past the transient scratch
+  int32_t* heirs = s.claim_list + s.cap;   // claims staged as heirs, in order
+  const int top0 = s.counters[kFreeTop];
+
+  // liveness of persistent slots; close marks
+  for (int i = tid; i < (s.S_p + 31) / 32; i += kPrepThreads) sh.live[i] = 0;
   __syncthreads();
-  for (int b = tid; b < s.NB; b += kPrepThreads) {
-    const int w = s.wslot[b];
-    if (w >= s.S_p) {
-      s.wslot[b] = -1;  // transient slots never outlive their step
-    } else if (w >= 0 && live_tag[b] != step) {
-      s.wslot[b] = -1;
-      s.free_stack[atomicAdd(&s.counters[kFreeTop], 1)] = w;
-    }
+  for (int i = tid; i < n_live; i += kPrepThreads) {
+    const int b = live[i];
+    const int w = b >= 0 && b < s.NB ? s.wslot[b] : -1;
+    if (w >= 0 && w < s.S_p) atomicOr(&sh.live[w >> 5], 1u << (w & 31));
   }
   for (int i = tid; i < n_tok; i += kPrepThreads) {
-    const int64_t sl = slots[i];
-    if (sl >= 0 && (sl & 127) == 127) close_tag[sl >> 7] = step;
+    const int b = slot_block(s, slots[i], 127);
+    if (b >= 0) close_tag[b] = step;
   }
   __syncthreads();
-  for (int i = tid; i < n_tok; i += kPrepThreads) {
-    const int64_t sl = slots[i];
-    if (sl < 0 || (sl & 127) != 0) continue;
-    const int b = (int)(sl >> 7);
-    if (atomicExch(&claim_tag[b], step) == step) continue;
-    int w = s.wslot[b];
-    if (w < 0) {
-      const bool closes = close_tag[b] == step;
-      if (closes) {  // opens and closes within the step: transient slot
-        const int t = atomicAdd(&s.counters[kTrans], 1);
-        if (t < s.S_t) w = s.S_p + t;
-      }
-      if (w < 0) {
-        const int top = atomicSub(&s.counters[kFreeTop], 1) - 1;
-        if (top >= 0) {
-          w = s.free_stack[top];
-        } else {
-          atomicAdd(&s.counters[kFreeTop], 1);
-          // No free persistent slot: stage in transient scratch and inherit
-          // the slot of a block closing this step.
-          const int t = closes ? s.S_t : atomicAdd(&s.counters[kTrans], 1);
-          if (t < s.S_t) {
-            w = s.S_p + t;
-            s.claim_list[s.cap + atomicAdd(&s.counters[kHeirs], 1)] = b;
-          } else {
-            atomicAdd(&s.counters[kErrStaging], 1);
-          }
+
+  // GC: transient slots end with their step; persistent slots of blocks not
+  // live go back on the free stack (pushed in block order)
+  const int freed = wg_compact(
+      s.NB, sh,
+      [&](int b) {
+        const int w = s.wslot[b];
+        if (w >= s.S_p) s.wslot[b] = -1;
+        if (w < 0 || w >= s.S_p || ((sh.live[w >> 5] >> (w & 31)) & 1u)) return -1;
+        s.wslot[b] = -1;
+        return w;
+      },
+      [&](int, int r, int w) { s.free_stack[top0 + r] = w; });
+  const int top = top0 + freed;
+
+  // claims (offset 0), one per block
+  const int n_cand = wg_compact(
+      n_tok, sh,
+      [&](int i) {
+        const int b = slot_block(s, slots[i], 0);
+        return b >= 0 && atomicExch(&claim_tag[b], step) != step ? b : -1;
+      },
+      [&](int, int r, int b) { tmp[r] = b; });
+  // blocks that open and close within the step: transient scratch in order
+  const int n_close_claims = wg_compact(
+      n_cand, sh,
+      [&](int i) {
+        const int b = tmp[i];
+        return s.wslot[b] < 0 && close_tag[b] == step ? b : -1;
+      },
+      [&](int, int r, int b) {
+        if (r < s.S_t)
+          s.wslot[b] = s.S_p + r;
+        else
+          late[r - s.S_t] = b;
+      });
+  const int trans0 = min(n_close_claims, s.S_t);
+  // blocks that stay open: the free stack from its top, then heirs in scratch
+  int errors = 0;
+  const int n_open_claims = wg_compact(
+      n_cand, sh,
+      [&](int i) {
+        const int b = tmp[i];
+        return s.wslot[b] < 0 && close_tag[b] != step ? b : -1;
+      },
+      [&](int, int r, int b) {
+        if (r < top) {
+          s.wslot[b] = s.free_stack[top - 1 - r];
+        } else if (trans0 + r - top < s.S_t) {
+          s.wslot[b] = s.S_p + trans0 + r - top;
+          heirs[r - top] = b;
         }
-      }
-    }
-    s.wslot[b] = w;
-    if (w >= 0) s.claim_list[atomicAdd(&s.counters[kClaims], 1)] = b;
+      });
+  const int n_heirs = min(max(n_open_claims - top, 0), s.S_t - trans0);
+  errors += max(n_open_claims - top, 0) - n_heirs;
+  // closing blocks the scratch could not hold take what the stack has left
+  const int n_late = n_close_claims - trans0;
+  for (int q = tid; q < n_late; q += kPrepThreads) {
+    const int d = n_open_claims + q;
+    if (d < top) s.wslot[late[q]] = s.free_stack[top - 1 - d];
   }
+  errors += max(n_late - max(top - n_open_claims, 0), 0);
   __syncthreads();
-  const int n_heirs = s.counters[kHeirs];
-  for (int i = tid; i < n_tok; i += kPrepThreads) {
-    const int64_t sl = slots[i];
-    if (sl < 0 || (sl & 127) != 127) continue;
-    const int b = (int)(sl >> 7);
-    if (atomicExch(&dedupe_tag[b], step) == step) continue;
-    const int w = s.wslot[b];
-    if (w < 0) continue;
-    const int c = atomicAdd(&s.counters[kCloses], 1);
-    s.close_list[c] = b;
-    int heir = -1;
-    if (w < s.S_p && n_heirs) {
-      const int d = atomicAdd(&s.counters[kDonors], 1);
-      if (d < n_heirs) heir = s.claim_list[s.cap + d];
-    }
-    s.close_list[s.cap + c] = heir;
-  }
-  __syncthreads();
-  if (tid == 0 && s.counters[kDonors] < n_heirs) atomicAdd(&s.counters[kErrStaging], n_heirs - s.counters[kDonors]);
-  const int n_claim = s.counters[kClaims];
+  const int n_claims = wg_compact(
+      n_cand, sh, [&](int i) { return s.wslot[tmp[i]] >= 0 ? tmp[i] : -1; },
+      [&](int, int r, int b) { s.claim_list[r] = b; });
+
+  // closes (offset 127), one per block holding staging; persistent donors
+  // hand their slot to the heirs in order
+  const int n_closes = wg_compact(
+      n_tok, sh,
+      [&](int i) {
+        const int b = slot_block(s, slots[i], 127);
+        return b >= 0 && atomicExch(&dedupe_tag[b], step) != step && s.wslot[b] >= 0 ? b : -1;
+      },
+      [&](int, int r, int b) {
+        s.close_list[r] = b;
+        s.close_list[s.cap + r] = -1;
+      });
+  const int n_donors = wg_compact(
+      n_closes, sh, [&](int c) { return s.wslot[s.close_list[c]] < s.S_p ? c : -1; },
+      [&](int, int d, int c) {
+        if (d < n_heirs) s.close_list[s.cap + c] = heirs[d];
+      });
+  errors += max(n_heirs - n_donors, 0);
+
+  // claimed blocks' records -> their staging, raw; freed overflow slots; page fill reset
   const int per = s.L * 2 * s.H;
-  for (int x = tid; x < n_claim * per; x += kPrepThreads) {
+  for (int x = tid; x < n_claims * per; x += kPrepThreads) {
     const int b = s.claim_list[x / per];
     const int r = x % per, layer = r / (2 * s.H), kvh = r % (2 * s.H);
     const int64_t idx = ((int64_t)layer * s.NB + b) * 2 * s.H + kvh;
@@ -241,6 +334,16 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
     s.rec_addr[idx] = reinterpret_cast<int64_t>(staging_addr(s, s.wslot[b], layer, kvh));
     s.rec_len[idx] = kRawVarLen;
     if (kvh == 0) s.fill[(int64_t)layer * s.NB + b] = 0;
+  }
+  if (tid == 0) {
+    const int popped = min(top, n_open_claims + n_late);
+    s.counters[kFreeTop] = top - popped;
+    s.counters[kTrans] = trans0 + n_heirs;
+    s.counters[kClaims] = n_claims;
+    s.counters[kCloses] = n_closes;
+    s.counters[kHeirs] = n_heirs;
+    s.counters[kDonors] = n_donors;
+    if (errors) s.counters[kErrStaging] += errors;
   }
 }
 
@@ -745,22 +848,27 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   }
 }
 
-// Closed blocks release their staging or pass it to their heir; the close
-// count is reset so a forward without a fresh prepare encodes nothing.
-__global__ void __launch_bounds__(kThreads) commit_kernel(Store s) {
+// commit: closed blocks hand their slot to their heir or push a persistent
+// slot back on the free stack (in close-list order); the close count is
+// reset so a forward without a fresh prepare encodes nothing.
+__global__ void __launch_bounds__(kPrepThreads) commit_kernel(Store s) {
+  __shared__ PrepShared sh;
   const int n = s.counters[kCloses];
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int b = s.close_list[i];
-    const int w = s.wslot[b];
-    const int heir = s.close_list[s.cap + i];
-    if (heir >= 0)
-      s.wslot[heir] = w;
-    else if (w >= 0 && w < s.S_p)
-      s.free_stack[atomicAdd(&s.counters[kFreeTop], 1)] = w;
-    s.wslot[b] = -1;
+  const int top = s.counters[kFreeTop];
+  const int pushed = wg_compact(
+      n, sh,
+      [&](int c) {
+        const int b = s.close_list[c], heir = s.close_list[s.cap + c];
+        const int w = s.wslot[b];
+        s.wslot[b] = -1;
+        if (heir >= 0) s.wslot[heir] = w;
+        return heir < 0 && w >= 0 && w < s.S_p ? w : -1;
+      },
+      [&](int, int r, int w) { s.free_stack[top + r] = w; });
+  if (threadIdx.x == 0) {
+    s.counters[kFreeTop] = top + pushed;
+    s.counters[kCloses] = 0;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) s.counters[kCloses] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1075,6 +1183,8 @@ extern "C" int fp_hbm_prepare(const fp_store_t* d, const int64_t* slot_mapping, 
   FP_CHECK(n_tok >= 0 && n_live >= 0, "negative token or live count");
   FP_CHECK(2 * n_tok <= 2 * d->list_cap, "block lists too small");
   FP_CHECK(n_live <= d->num_blocks, "more live blocks than blocks");
+  FP_CHECK(d->staging_slots <= 32LL * kLiveWords, "too many persistent staging slots (at most 262144)");
+  FP_CHECK(n_tok < (1LL << 30), "too many tokens in one step");
   const Store s = make_store(d);
   hipLaunchKernelGGL(prepare_kernel, dim3(1), dim3(kPrepThreads), 0, stream, s, slot_mapping, (int)n_tok, live,
                      (int)n_live, (int32_t)step);
@@ -1157,7 +1267,7 @@ extern "C" int fp_hbm_encode_ordered(const fp_store_t* d, const uint8_t* rank_of
 extern "C" int fp_hbm_commit(const fp_store_t* d, fp_stream_t stream) {
   if (check_store(d)) return -1;
   const Store s = make_store(d);
-  hipLaunchKernelGGL(commit_kernel, dim3(1), dim3(kThreads), 0, stream, s);
+  hipLaunchKernelGGL(commit_kernel, dim3(1), dim3(kPrepThreads), 0, stream, s);
   FP_LAUNCH_CHECK();
   return 0;
 }

@@ -1,107 +1,110 @@
-"""Version-pinned adaptation of vLLM's V2 model runner.
+"""The one vLLM release this integration patches, and the patch itself.
 
-Reference: fragpack/integrations/vllm/compat.py.  Attention backends never see
-the scheduler output, but the store needs each step's open blocks; the
-wrapper installed here feeds :class:`OpenBlocks` before every real model step.
-That is a runtime patch of one vLLM release, so the release is checked first.
+Reference interface: fragpack/integrations/vllm/compat.py
+(``SUPPORTED_VLLM_VERSION``, ``require_supported_vllm``, ``install_tracker``,
+``installed_tracker``).  Attention backends never see the scheduler output,
+but the store needs each step's open blocks (:class:`OpenBlocks`), so the V2
+model runner's ``execute_model`` is wrapped to feed the tracker before every
+real step.  Wrapping a method of one release is version-specific: the release
+is checked before anything is touched.
 
-The reference pins the CUDA wheel "0.30.0+cu129".  This build runs on ROCm, so
-it pins the same release built for ROCm: public version "0.30.0" with a local
-label that starts with "rocm" (e.g. "0.30.0+rocm700").  CUDA wheels, other
-releases and unlabelled source builds are rejected.  Checking the version
-imports neither torch nor vLLM.
+The reference pins the CUDA wheel "0.30.0+cu129"; this build runs on ROCm and
+pins the same release's ROCm builds: public version "0.30.0" with a local
+label starting "rocm" (e.g. "0.30.0+rocm700").  Checking the version imports
+neither torch nor vLLM.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 import functools
 from importlib import metadata
-from typing import TYPE_CHECKING, Any
+from typing import TYPE_CHECKING, Any, Callable
 
 if TYPE_CHECKING:
     from fragpack_amd.integrations.vllm.lifecycle import OpenBlocks
 
-SUPPORTED_VLLM_RELEASE = "0.30.0"
-SUPPORTED_LOCAL_PREFIX = "rocm"
-SUPPORTED_VLLM_VERSION = f"{SUPPORTED_VLLM_RELEASE}+{SUPPORTED_LOCAL_PREFIX}*"
-_installed_tracker: OpenBlocks | None = None
+
+@dataclass(frozen=True)
+class _Pin:
+    release: str
+    local_prefix: str
+
+    def __str__(self) -> str:
+        return f"{self.release}+{self.local_prefix}*"
+
+    def admits(self, version: str) -> bool:
+        public, plus, local = version.partition("+")
+        return public == self.release and bool(plus) and local.startswith(self.local_prefix)
 
 
-def _supported(version: str) -> bool:
-    release, _, local = version.partition("+")
-    return release == SUPPORTED_VLLM_RELEASE and local.startswith(SUPPORTED_LOCAL_PREFIX)
+_PIN = _Pin("0.30.0", "rocm")
+SUPPORTED_VLLM_VERSION = str(_PIN)
+
+
+class _RunnerPatch:
+    """The installed wrapper: which tracker it feeds."""
+
+    tracker: OpenBlocks | None = None
+
+    @staticmethod
+    def wrap(step: Callable[..., Any], tracker: OpenBlocks) -> Callable[..., Any]:
+        @functools.wraps(step)
+        def execute_model(runner: Any, scheduler_output: Any, *args: Any, **kwargs: Any) -> Any:
+            if not kwargs.get("dummy_run", False):  # profiling / warm-up runs carry no real requests
+                tracker.update(scheduler_output)
+            return step(runner, scheduler_output, *args, **kwargs)
+
+        return execute_model
 
 
 def require_supported_vllm(*, use_v2_model_runner: bool | None = None) -> str:
-    """Reject an absent or unsupported vLLM distribution, or a non-V2 runner.
+    """The installed vLLM version, if it is the pinned release's ROCm build.
 
     Args:
         use_v2_model_runner: The resolved runner choice; None (plugin
             discovery) checks the distribution only.
 
-    Returns:
-        The installed distribution version.
-
     Raises:
-        RuntimeError: vLLM is not installed, or its version is not the pinned
-            release for ROCm.
+        RuntimeError: vLLM is absent or is another build or release.
         ValueError: ``use_v2_model_runner`` is False.
     """
     try:
-        installed = metadata.version("vllm")
+        found = metadata.version("vllm")
     except metadata.PackageNotFoundError as exc:
         raise RuntimeError(f"FragPack requires vllm=={SUPPORTED_VLLM_VERSION}; vLLM is not installed") from exc
-    if not _supported(installed):
-        raise RuntimeError(
-            f"FragPack requires vllm=={SUPPORTED_VLLM_VERSION}; found {installed}. "
-            "Its V2 lifecycle adapter is release-specific."
-        )
-    if use_v2_model_runner is not None and not use_v2_model_runner:
+    if not _PIN.admits(found):
+        raise RuntimeError(f"FragPack requires vllm=={SUPPORTED_VLLM_VERSION}, found {found}: the runner patch "
+                           "is release-specific")
+    if use_v2_model_runner is False:
         raise ValueError("FragPack attention needs the V2 model runner")
-    return installed
+    return found
 
 
 def install_tracker(tracker: OpenBlocks, *, use_v2_model_runner: bool) -> None:
-    """Wrap ``GPUModelRunner.execute_model`` once so that every real step
-    updates ``tracker`` before the model runs (dummy runs pass straight
-    through).
+    """Feed ``tracker`` from every real model step (idempotent per tracker).
 
-    Args:
-        tracker: The worker's block tracker, shared with the backend.
-        use_v2_model_runner: Must be True.
+    Call during worker initialisation, before the model runs.
 
     Raises:
-        RuntimeError: Unsupported distribution, or a different tracker is
-            already installed (the backend would otherwise read a stale one).
+        RuntimeError: Unsupported vLLM, or another tracker is already installed
+            (the backend would read a stale mirror).
         ValueError: The runner is not V2.
-
-    Repeating the call with the installed tracker does nothing.  Call during
-    worker initialisation, before model execution starts.
     """
-    global _installed_tracker
     require_supported_vllm(use_v2_model_runner=use_v2_model_runner)
-    if _installed_tracker is tracker:
+    if _RunnerPatch.tracker is tracker:
         return
-    if _installed_tracker is not None:
-        raise RuntimeError("FragPack V2 lifecycle adapter already has a tracker")
-
+    if _RunnerPatch.tracker is not None:
+        raise RuntimeError("FragPack's V2 runner patch already has a tracker")
     from vllm.v1.worker.gpu.model_runner import GPUModelRunner
 
-    wrapped = GPUModelRunner.execute_model
-
-    @functools.wraps(wrapped)
-    def execute_model(self: Any, scheduler_output: Any, *args: Any, **kwargs: Any) -> Any:
-        if not kwargs.get("dummy_run", False):
-            tracker.update(scheduler_output)
-        return wrapped(self, scheduler_output, *args, **kwargs)
-
-    GPUModelRunner.execute_model = execute_model
-    _installed_tracker = tracker
+    GPUModelRunner.execute_model = _RunnerPatch.wrap(GPUModelRunner.execute_model, tracker)
+    _RunnerPatch.tracker = tracker
 
 
 def installed_tracker() -> OpenBlocks | None:
-    """The tracker the runner wrapper feeds, or None before installation."""
-    return _installed_tracker
+    """The tracker the runner patch feeds, or None before installation."""
+    return _RunnerPatch.tracker
 
 
 __all__ = ["SUPPORTED_VLLM_VERSION", "install_tracker", "installed_tracker", "require_supported_vllm"]

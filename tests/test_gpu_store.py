@@ -1,21 +1,19 @@
-"""HBM store steps (prepare / write / encode / commit) vs the oracle.
+"""The GPU store (HbmKvStore over libfragpack_hip.so) driven by a simulated
+serving engine, checked against the CPU store model and the CPU oracle.
 
-Follows the reference's store contract (tests/gpu/test_fragpack_hbm_store.py
-in the reference repo): a few serving steps of a small batch through the
-public API, then
-
-* every closed block's coded records are byte-identical to the oracle's
-  ``encode_record`` of the written tokens and packed disjointly in their
-  block-layer page; raw records (the one incompressible "WIDE" record, and
-  with a tight page the records that no longer fit) hold the written KV;
-* counters: encoded / fallbacks / spills exact, no staging or overflow loss;
-* gather returns the written tokens bit-exactly (zeros for a never-written
-  block), decode attention over coded, raw and still-open blocks matches
-  the fp32 reference for GQA 8/4/2/1;
-* a request whose chunk closes its open block and opens a new tail inherits
-  the closing block's staging slot;
-* block blobs exported from one store install into another (same bytes,
-  overflow accounting) and corrupt or foreign blobs are rejected untouched.
+The contract is the reference's (fragpack/ops/hbm_kv.py:1-47, hbm_kv.cu):
+after every ``prepare`` and ``commit`` the store's bookkeeping -- which
+staging slot each block holds, the free stack, the claim / close / heir
+lists and the counters -- equals ``oracle.store_model.StoreModel`` exactly
+(the kernels build every list in input order, so the state is a function of
+the steps); after the steps every closed block's records are the oracle
+codec's bytes, placed disjointly in their page or raw in the overflow pool,
+gather returns the written KV bit for bit, and decode attention over coded,
+raw and open blocks matches fp32 softmax attention.  Scenarios: GC of a
+finished request's slot, a tight page (spills), an incompressible record
+(fallback), a chunk that closes its open block and opens a new one while
+staging is full (heir inherits the donor's slot), staging and overflow
+exhaustion surfacing as StoreError, and block blobs moving between stores.
 """
 
 from __future__ import annotations
@@ -23,330 +21,376 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from oracle import oracle
+from oracle.store_model import StoreModel
 from tests import kvgen
 from tests.conftest import gpu_available
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 
-L, H, D, T = 2, 2, 128, 128
-GQA = 8
-HQ = H * GQA
-NB = 12
-SCALE = D ** -0.5
-WIDE = (9, 0, 0, 1)  # (block, layer, kv, head) made incompressible
-DENSE = 22528
-RAW = 32768
+T, D = 128, 128
+DENSE, RAW = 22528, 32768
 
 
-def _bits(x):
-    return kvgen.bf16_bits(x)
-
-
-def _bf16(bits):
+def _dev_bits(bits):
     import torch
 
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch.bfloat16)
 
 
-def _overflow_used(store, records):
-    bits = np.unpackbits(store.ovf_bits.cpu().numpy().view(np.uint8))
-    return int(bits.sum()) - (bits.size - records)
+class SimEngine:
+    """A serving engine in miniature: requests own block lists taken from a
+    pool (lowest id first); each step schedules some tokens per request and
+    runs prepare -> (write, encode) per layer -> commit on the GPU store and
+    on the store model, keeping the written KV on the host."""
 
-
-class Harness:
-    def __init__(self, seed: int, page: int, overflow_records: int = 16, staging_slots: int = 3):
+    def __init__(self, seed, layers=2, heads=2, blocks=12, page=None, staging=3, overflow=16, noisy=()):
         import torch
 
-        from fragpack_amd.compression.attn_tables import device_tables
-        from fragpack_amd.ops.hbm_kv import HbmKvStore
-        from oracle import oracle
+        from fragpack_amd.compression.attn_tables import calibrate, device_tables
+        from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
 
         self.rng = np.random.default_rng(seed)
-        self.page = page
-        cal = _bits(self.rng.standard_normal((L, 2, H, 4 * T, D)) * 0.5)
-        self.table = np.empty((L, 2, H, 22), np.uint8)
-        for idx in np.ndindex(L, 2, H):
-            self.table[idx] = oracle.calibrate_table((cal[idx] >> 8).astype(np.uint8))
-        # garbage, like an engine's uninitialised cache
-        self.caches = [torch.randint(0, 256, (NB, page), dtype=torch.uint8, device="cuda") for _ in range(L)]
-        self.store = HbmKvStore(self.caches, H, device_tables(self.table, torch.device("cuda")), max_tokens=1024,
-                                staging_slots=staging_slots, overflow_records=overflow_records)
-        self.overflow_records = overflow_records
-        self.ref = np.zeros((L, 2, NB, T, H, D), np.uint16)
+        self.L, self.H, self.NB = layers, heads, blocks
+        self.page = page or page_bytes(heads)
+        dump = kvgen.bf16_bits(self.rng.standard_normal((6, layers, 2, T, heads, D)) * 0.5)
+        self.table = calibrate(dump)  # [L, 2, H, 22]
+        # an engine's cache starts as garbage
+        self.caches = [torch.randint(0, 256, (blocks, self.page), dtype=torch.uint8, device="cuda")
+                       for _ in range(layers)]
+        self.max_tokens = 1024
+        self.store = HbmKvStore(self.caches, heads, device_tables(self.table, torch.device("cuda")),
+                                max_tokens=self.max_tokens, staging_slots=staging, overflow_records=overflow)
+        self.model = StoreModel(layers, blocks, heads, staging, self.store.scratch.shape[0],
+                                self.store.staging.data_ptr(), self.store.scratch.data_ptr())
+        self.kv = np.zeros((layers, 2, blocks, T, heads, D), np.uint16)  # written KV by block
+        self.reqs: dict[str, list] = {}  # name -> [blocks, computed]
+        self.pool = list(range(blocks))
+        self.noisy = set(noisy)  # (block, layer, kv, head) written with values too spread to code
+        self.filled: dict[int, int] = {}
+        self.heirs_seen = 0
 
-    def step(self, rows, live):
-        """One engine step; a row is (blocks, first position, token count)."""
+    def _take(self, n):
+        got = sorted(self.pool)[:n]
+        for b in got:
+            self.pool.remove(b)
+        return got
+
+    def finish(self, name):
+        blocks, _ = self.reqs.pop(name)
+        self.pool.extend(blocks)
+        for b in blocks:
+            self.filled.pop(b, None)
+
+    def step(self, sched):
+        """``sched``: (request, tokens) pairs; unknown requests are admitted."""
         import torch
 
-        slots = [blocks[q // T] * T + q % T for blocks, start, n in rows for q in range(start, start + n)]
-        n = len(slots)
+        live = []
+        for name, (blocks, computed) in self.reqs.items():
+            if computed % T and computed // T < len(blocks):
+                live.append(blocks[computed // T])
+        slots, pos = [], []
+        closes = 0
+        for name, n in sched:
+            blocks, computed = self.reqs.setdefault(name, [[], 0])
+            need = -(-(computed + n) // T) - len(blocks)
+            blocks.extend(self._take(need))
+            for p in range(computed, computed + n):
+                slots.append(blocks[p // T] * T + p % T)
+                pos.append((blocks[p // T], p % T))
+            closes += (computed + n) // T - computed // T
+            self.reqs[name][1] = computed + n
         slot_t = torch.tensor(slots, dtype=torch.int64, device="cuda")
-        closes = sum((st + cnt) // T - st // T for _, st, cnt in rows)
-        self.store.prepare(slot_t, n, np.array(live, np.int32))
-        blk, off = np.array(slots) // T, np.array(slots) % T
-        for layer in range(L):
-            kv = _bits(self.rng.standard_normal((2, n, H, D)) * 0.5)
-            hit = blk == WIDE[0]
-            if layer == WIDE[1] and hit.any():
-                wide = np.exp2(self.rng.uniform(-40, 4, (int(hit.sum()), D)))
-                kv[WIDE[2], hit, WIDE[3]] = _bits(wide)
-            self.ref[layer, :, blk, off] = kv.transpose(1, 0, 2, 3)
-            # K / V as strided slices of one fused qkv row, like a serving engine
-            qkv = torch.empty(n, HQ + 2 * H, D, dtype=torch.bfloat16, device="cuda")
-            qkv[:, HQ : HQ + H] = _bf16(kv[0])
-            qkv[:, HQ + H :] = _bf16(kv[1])
-            self.store.write(layer, qkv[:, HQ : HQ + H], qkv[:, HQ + H :], slot_t)
+        self.store.prepare(slot_t, len(slots), np.array(live, np.int32))
+        self.model.prepare(slots, live)
+        self.heirs_seen += len(self.model.heirs)
+        self.check_bookkeeping(claims=True)
+        blk = np.array([b for b, _ in pos])
+        off = np.array([o for _, o in pos])
+        n = len(slots)
+        for layer in range(self.L):
+            kv = kvgen.bf16_bits(self.rng.standard_normal((2, n, self.H, D)) * 0.5)
+            for b, lyr, k, h in self.noisy:
+                hit = blk == b
+                if lyr == layer and hit.any():
+                    # finite values over ~44 binary orders of magnitude: high bytes spread too wide to code
+                    mag = np.exp2(self.rng.uniform(-40, 4, (int(hit.sum()), D)))
+                    kv[k, hit, h] = kvgen.bf16_bits(mag * self.rng.choice([-1.0, 1.0], mag.shape))
+            self.kv[layer, :, blk, off] = kv.transpose(1, 0, 2, 3)
+            # K / V as strided views of a fused qkv row, as an engine hands them over
+            qkv = torch.empty(n, 3 * self.H, D, dtype=torch.bfloat16, device="cuda")
+            qkv[:, self.H : 2 * self.H] = _dev_bits(kv[0])
+            qkv[:, 2 * self.H :] = _dev_bits(kv[1])
+            self.store.write(layer, qkv[:, self.H : 2 * self.H], qkv[:, 2 * self.H :], slot_t)
             self.store.encode(layer, closes)
         self.store.commit()
+        self.model.commit()
+        self.check_bookkeeping(claims=False)
+        for b, o in pos:
+            self.filled[b] = max(self.filled.get(b, 0), o + 1)
 
-    def check_arena(self, blocks):
-        """Closed blocks' records vs the oracle; returns (fallbacks, spills)."""
-        from oracle import oracle
+    # ------------------------------------------------------------------ checks
+    def check_bookkeeping(self, claims):
+        st, m = self.store, self.model
+        top = int(st.counters[0])
+        assert np.array_equal(st.wslot.cpu().numpy(), m.wslot), "staging slot per block"
+        assert st.free_stack[:top].cpu().tolist() == m.free_stack, "free stack"
+        got = st.counters.cpu().numpy()
+        for i in (0, 1, 2, 3, 4, 9, 10):
+            assert got[i] == m.counters[i], f"counter {i}: {got[i]} vs {m.counters[i]}"
+        # every persistent slot is held by one block or free, exactly once
+        held = [int(w) for w in m.wslot if 0 <= w < m.staging_slots]
+        assert sorted(held + m.free_stack) == list(range(m.staging_slots))
+        if not claims:
+            return
+        cap = st.claim_list.numel() // 2
+        assert st.claim_list[: len(m.claims)].cpu().tolist() == m.claims
+        cl = st.close_list.cpu().numpy()
+        assert [(int(cl[c]), int(cl[cap + c])) for c in range(len(m.closes))] == m.closes
+        addr = st.rec_addr.cpu().numpy().reshape(self.L, self.NB, -1)
+        ln = st.rec_len.cpu().numpy().reshape(self.L, self.NB, -1)
+        for (layer, b, kvh), a in m.claimed_records().items():
+            assert addr[layer, b, kvh] == a and ln[layer, b, kvh] == RAW - DENSE
 
+    def check_records(self, blocks):
+        """Closed blocks' records vs the oracle codec; returns (fallbacks, spills)."""
         addr = self.store.rec_addr.cpu().numpy()
         length = self.store.rec_len.cpu().numpy()
-        overflow = self.store.overflow.cpu().numpy().reshape(-1)
-        ovf_base = self.store.overflow.data_ptr()
+        pool = self.store.overflow.cpu().numpy().reshape(-1)
+        pool0 = self.store.overflow.data_ptr()
         fallbacks = spills = 0
-        for b in blocks:
-            for layer in range(L):
-                arena = self.caches[layer].cpu().numpy().reshape(-1)
-                page = self.caches[layer].data_ptr() + b * self.page
-                used = []
-                for kv in range(2):
-                    for h in range(H):
-                        ref = self.ref[layer, kv, b, :, h]
-                        table = self.table[layer, kv, h]
-                        want = oracle.encode_record(ref, table, kv)
-                        a = int(addr[layer, b, kv, h])
-                        if ovf_base <= a < ovf_base + overflow.size:
-                            got = overflow[a - ovf_base :][:RAW]
-                            np.testing.assert_array_equal(oracle.decode_record(got.tobytes(), table, kv), ref)
-                            assert int(length[layer, b, kv, h]) == RAW - DENSE
+        for layer in range(self.L):
+            arena = self.caches[layer].cpu().numpy().reshape(-1)
+            base = self.caches[layer].data_ptr()
+            for b in blocks:
+                spans = []
+                for k in range(2):
+                    for h in range(self.H):
+                        tok = self.kv[layer, k, b, :, h]
+                        want = oracle.encode_record(tok, self.table[layer, k, h], k)
+                        a = int(addr[layer, b, k, h])
+                        if pool0 <= a < pool0 + pool.size:
+                            assert int(length[layer, b, k, h]) == RAW - DENSE
+                            assert pool[a - pool0 : a - pool0 + RAW].tobytes() == oracle.raw_record(tok, k)
                             if len(want) == RAW:
                                 fallbacks += 1
-                                assert (b, layer, kv, h) == WIDE
                             else:
                                 spills += 1
                             continue
-                        n = len(want)
-                        assert n < RAW, (b, layer, kv, h)
-                        assert a % 16 == 0 and page <= a <= page + self.page - n
-                        assert DENSE + int(length[layer, b, kv, h]) == n
-                        o = a - self.caches[layer].data_ptr()
-                        assert arena[o : o + n].tobytes() == want, (b, layer, kv, h)
-                        used.append((a, a + n))
-                used.sort()
-                assert all(e <= s for (_, e), (s, _) in zip(used[:-1], used[1:]))
+                        assert len(want) < RAW, ("a record that does not code is not in the pool", b, layer, k, h)
+                        o = a - base
+                        assert o % 16 == 0 and b * self.page <= o <= (b + 1) * self.page - len(want)
+                        assert DENSE + int(length[layer, b, k, h]) == len(want)
+                        assert arena[o : o + len(want)].tobytes() == want, (b, layer, k, h)
+                        spans.append((o, o + len(want)))
+                spans.sort()
+                assert all(e <= s for (_, e), (s, _) in zip(spans, spans[1:])), "records overlap in a page"
         return fallbacks, spills
 
-    def check_gather(self, filled):
+    def check_gather(self, filled=None):
         import torch
 
+        filled = dict(filled or self.filled)
         blocks = sorted(filled)
-        src = torch.tensor(blocks, dtype=torch.int32, device="cuda")
-        wk = torch.empty(len(blocks), T, H, D, dtype=torch.bfloat16, device="cuda")
+        ids = torch.tensor(blocks, dtype=torch.int32, device="cuda")
+        wk = torch.empty(len(blocks), T, self.H, D, dtype=torch.bfloat16, device="cuda")
         wv = torch.empty_like(wk)
-        for layer in range(L):
-            self.store.gather(layer, src, wk, wv)
+        for layer in range(self.L):
+            self.store.gather(layer, ids, wk, wv)
             got = [x.view(torch.int16).cpu().numpy().view(np.uint16) for x in (wk, wv)]
             for i, b in enumerate(blocks):
-                n = filled[b]
-                for kv in range(2):
-                    np.testing.assert_array_equal(got[kv][i, :n], self.ref[layer, kv, b, :n], err_msg=f"{b}")
+                for k in range(2):
+                    np.testing.assert_array_equal(got[k][i, : filled[b]], self.kv[layer, k, b, : filled[b]])
 
-    def check_decode(self, tables, seqs, group=GQA):
+    def check_decode(self, names, group):
         import torch
 
         from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
 
-        B = len(seqs)
-        width = max(len(t) for t in tables)
-        bt = np.zeros((B, width), np.int32)
+        tables = [self.reqs[r][0] for r in names]
+        lens = [self.reqs[r][1] for r in names]
+        B, H = len(names), self.H
+        bt = np.zeros((B, max(len(t) for t in tables)), np.int32)
         for i, t in enumerate(tables):
             bt[i, : len(t)] = t
-        block_table = torch.from_numpy(bt).cuda()
-        seq_lens = torch.tensor(seqs, dtype=torch.int32, device="cuda")
+        bt_t = torch.from_numpy(bt).cuda()
+        lens_t = torch.tensor(lens, dtype=torch.int32, device="cuda")
         sms = torch.cuda.get_device_properties(0).multi_processor_count
-        for units in (decode_units(B, H, sms), B, B + 1):
-            opart, ml, plan = workspace_elems(H, units)
-            ws = (torch.empty(opart, device="cuda"), torch.empty(ml, device="cuda"),
-                  torch.empty(plan, dtype=torch.int32, device="cuda"))
-            for layer in range(L):
-                q = torch.randn(B, H * group, D, dtype=torch.bfloat16, device="cuda")
+        for units in (decode_units(B, H, sms), B):
+            ws = tuple(torch.empty(n, dtype=dt, device="cuda")
+                       for n, dt in zip(workspace_elems(H, units), (torch.float32, torch.float32, torch.int32)))
+            for layer in range(self.L):
+                q = torch.randn(B, H * group, D, device="cuda").to(torch.bfloat16)
                 out = torch.empty_like(q)
-                decode_attention(q, RecordTables(*self.store.layer_tables(layer)), block_table, seq_lens, SCALE,
-                                 units, out, ws, layer == 0)
-                kvf = _bf16(self.ref[layer]).float()  # [2, NB, T, H, D]
-                ref = torch.empty(B, H * group, D, device="cuda")
-                for i, (t, s) in enumerate(zip(tables, seqs)):
-                    pg = torch.tensor(t, device="cuda")
-                    for h in range(H):
-                        k = kvf[0, pg, :, h].reshape(-1, D)[:s]
-                        v = kvf[1, pg, :, h].reshape(-1, D)[:s]
-                        qh = q[i, group * h : group * (h + 1)].float()
-                        ref[i, group * h : group * (h + 1)] = torch.softmax(qh @ k.T * SCALE, -1) @ v
-                torch.testing.assert_close(out.float(), ref, atol=2e-2, rtol=1e-2)
+                decode_attention(q, RecordTables(*self.store.layer_tables(layer)), bt_t, lens_t, D ** -0.5, units,
+                                 out, ws, layer == 0)
+                kvf = _dev_bits(self.kv[layer]).float()  # [2, NB, T, H, D]
+                for i in range(B):
+                    pg = torch.tensor(tables[i], device="cuda")
+                    k = kvf[0, pg].reshape(-1, H, D)[: lens[i]]
+                    v = kvf[1, pg].reshape(-1, H, D)[: lens[i]]
+                    qi = q[i].float().view(H, group, D)
+                    p = torch.softmax(torch.einsum("hgd,thd->hgt", qi, k) * D ** -0.5, -1)
+                    ref = torch.einsum("hgt,thd->hgd", p, v).reshape(H * group, D)
+                    torch.testing.assert_close(out[i].float(), ref, atol=2e-2, rtol=1e-2)
 
 
-def _page_bytes():
-    from fragpack_amd.ops.hbm_kv import page_bytes
-
-    return page_bytes(H)
+def _serve(eng):
+    """Prefills of 300 / 256 / 10 tokens, then decodes; the 10-token request
+    finishes and a new one is admitted (its slot must come from GC)."""
+    eng.step([("a", 300), ("b", 256), ("c", 10)])
+    eng.step([("a", 84), ("b", 1), ("c", 1)])
+    eng.finish("c")
+    eng.step([("a", 1), ("b", 1), ("d", 10)])
+    eng.step([("a", 1), ("b", 1), ("d", 1)])
 
 
 @pytest.mark.parametrize("tight", [False, True])
-def test_store_steps_match_oracle(tight):
-    page = 2 * H * DENSE - 16 if tight else _page_bytes()
-    spills = 5 * L - 1 if tight else 0  # a tight page holds 3 of a block-layer's 4 records
-    h = Harness(0, page)
-    a, b, c, d = [0, 1, 4, 5], [8, 9, 10], [2], [3]
-    print("prefill step", flush=True)
-    h.step([(a, 0, 300), (b, 0, 256), (c, 0, 10)], a + b + c)
-    h.step([(a, 300, 84), (b, 256, 1), (c, 10, 1)], a + b + c)
+def test_serving_steps_match_model_and_oracle(tight):
     import torch
 
+    from fragpack_amd.ops.hbm_kv import page_bytes
+
+    H = 2
+    # a tight page holds 3 of a block-layer's 4 records: one spills per block-layer
+    page = 2 * H * DENSE - 16 if tight else page_bytes(H)
+    eng = SimEngine(0, heads=H, page=page, noisy={(3, 0, 0, 1)})
+    _serve(eng)
     torch.cuda.synchronize()
-    assert h.check_arena([0, 1, 4, 8, 9]) == (1, spills)
-    # C finished: GC must free block 2's slot or D / A's claims overflow staging
-    h.step([(a, 384, 1), (b, 257, 1), (d, 0, 10)], a + b + d)
-    h.step([(a, 385, 1), (b, 258, 1), (d, 10, 1)], a + b + d)
-    torch.cuda.synchronize()
-    st = h.store.stats()
-    assert st.encoded == 5 * L * 2 * H
-    assert st.fallbacks == 1 + spills and st.spills == spills
-    assert st.err_staging == 0 and st.err_overflow == 0
-    # block 11 was never written: reads as zeros, not arena garbage
-    h.check_gather({0: T, 1: T, 4: T, 5: 2, 8: T, 9: T, 10: 3, 3: 11, 11: T})
-    for group in (GQA, 4, 2, 1):
+    closed = [b for b, n in eng.filled.items() if n == T]
+    assert len(closed) == 5
+    fallbacks, spills = eng.check_records(closed)
+    assert fallbacks == 1 and spills == (len(closed) * eng.L - 1 if tight else 0)
+    st = eng.store.stats()
+    assert st.encoded == len(closed) * eng.L * 2 * H
+    assert (st.fallbacks, st.spills, st.err_staging, st.err_overflow) == (fallbacks + spills, spills, 0, 0)
+    eng.check_gather()
+    for group in (8, 4, 2, 1):
         print("decode group", group, flush=True)
-        h.check_decode([a, b, d, [11]], [386, 259, 11, T], group)
+        eng.check_decode(["a", "b", "d"], group)
 
 
-def test_chunk_reopening_tail_inherits_closing_slot():
+def test_closing_chunk_hands_its_slot_to_the_new_tail():
+    """With every persistent slot held, a chunk that fills a request's open
+    block and opens the next one stages the new tail as an heir, which takes
+    the closing block's slot at commit (hbm_kv.py:24-29)."""
     import torch
 
-    h = Harness(1, _page_bytes(), staging_slots=2)
-    a, b = [0, 1, 2], [3, 4, 5]
-    h.step([(a, 0, 200), (b, 0, 200)], [])
-    h.step([(a, 200, 100), (b, 200, 100)], [1, 4])
+    eng = SimEngine(1, staging=2)
+    eng.step([("a", 200), ("b", 200)])
+    eng.step([("a", 100), ("b", 100)])  # each closes block 1 and opens block 2
+    assert eng.heirs_seen == 2
     torch.cuda.synchronize()
-    assert h.store.stats().err_staging == 0
-    assert h.check_arena([0, 1, 3, 4]) == (0, 0)
-    h.check_gather({2: 44, 5: 44})
-    h.step([(a, 300, 1), (b, 300, 1)], [2, 5])
-    h.step([(a, 301, 83), (b, 301, 83)], [2, 5])
+    assert eng.store.stats().err_staging == 0
+    eng.step([("a", 1), ("b", 1)])
+    eng.step([("a", 83), ("b", 83)])
+    eng.step([("a", 250), ("b", 250)])  # closes a block, fills one, opens another
     torch.cuda.synchronize()
-    st = h.store.stats()
-    assert st.err_staging == 0 and st.err_overflow == 0
-    assert st.encoded == 6 * L * 2 * H
-    assert h.check_arena([0, 1, 2, 3, 4, 5]) == (0, 0)
-    h.check_gather({b: T for b in range(6)})
-    h.check_decode([a, b], [384, 384])
+    st = eng.store.stats()
+    assert (st.err_staging, st.err_overflow) == (0, 0)
+    closed = sorted(b for b, n in eng.filled.items() if n == T)
+    assert eng.check_records(closed) == (0, 0)
+    eng.check_gather()
+    eng.check_decode(["a", "b"], 8)
 
 
-SRC, DST = [0, 1, 4, 8, 9], [6, 7, 2, 3, 9]
+def test_staging_and_overflow_exhaustion_surface():
+    from fragpack_amd.ops.hbm_kv import StoreError
+
+    eng = SimEngine(3, staging=1)
+    eng.step([("a", 10), ("b", 10)])  # two open blocks, one slot
+    with pytest.raises(StoreError, match="staging"):
+        eng.store.stats()
+    eng = SimEngine(3, heads=2, page=2 * 2 * DENSE - 16, overflow=2)
+    eng.step([("a", 384)])  # 3 closed blocks x 2 layers: 6 spills, 2 slots
+    with pytest.raises(StoreError, match="overflow"):
+        eng.store.stats()
 
 
-def _prefill(h):
-    a, b, c = [0, 1, 4, 5], [8, 9, 10], [2]
-    h.step([(a, 0, 300), (b, 0, 256), (c, 0, 10)], a + b + c)
-    h.step([(a, 300, 84), (b, 256, 1), (c, 10, 1)], a + b + c)
-
-
-def _export(h, blocks):
+# ---------------------------------------------------------------- block blobs
+def _export(eng, blocks):
     import torch
 
-    stride = h.store.blob_stride
+    stride = eng.store.blob_stride
     out = torch.zeros(len(blocks) * stride, dtype=torch.uint8, device="cuda")
     ids = torch.tensor(blocks, dtype=torch.int32, device="cuda")
-    lengths = h.store.export_blocks(ids, out, stride).cpu().tolist()
-    return out, lengths
+    return out, eng.store.export_blocks(ids, out, stride).cpu().tolist()
 
 
-def _import(h, src, offsets, blocks):
+def _import(eng, src, offsets, blocks):
     import torch
 
     off = torch.tensor(offsets, dtype=torch.int64, device="cuda")
     ids = torch.tensor(blocks, dtype=torch.int32, device="cuda")
-    return h.store.import_blocks(src, off, ids).cpu().tolist()
+    return eng.store.import_blocks(src, off, ids).cpu().tolist()
+
+
+def _overflow_in_use(eng):
+    bits = np.unpackbits(eng.store.ovf_bits.cpu().numpy().view(np.uint8))
+    return int(bits.sum()) - (bits.size - eng.store.overflow.shape[0])
 
 
 @pytest.mark.parametrize("tight", [False, True])
-def test_blob_round_trip(tight):
+def test_blobs_move_closed_blocks_between_stores(tight):
     import torch
 
     from fragpack_amd.compression import attn_page as ap
+    from fragpack_amd.ops.hbm_kv import page_bytes
 
-    page = 2 * H * DENSE - 16 if tight else _page_bytes()
-    spills = 5 * L - 1 if tight else 0
-    src = Harness(0, page)
-    _prefill(src)
-    blobs, lengths = _export(src, SRC)
+    H = 2
+    page = 2 * H * DENSE - 16 if tight else page_bytes(H)
+    src = SimEngine(0, heads=H, page=page, noisy={(3, 0, 0, 1)})
+    _serve(src)
+    closed = sorted(b for b, n in src.filled.items() if n == T)
+    blobs, lengths = _export(src, closed)
     stride = src.store.blob_stride
-    assert stride == ap.blob_slot_bytes(L, H)
-    head = ap.blob_head_bytes(L, H)
+    assert stride == ap.blob_slot_bytes(src.L, H)
+    head = ap.blob_head_bytes(src.L, H)
     rec_len = src.store.rec_len.cpu().numpy()
-    for b, n in zip(SRC, lengths):
+    for b, n in zip(closed, lengths):
         body = sum(DENSE + int(v) for v in rec_len[:, b].ravel())
         assert n == -(-(head + body) // ap.BLOB_ALIGN) * ap.BLOB_ALIGN <= stride
-    # blob header fields (hbm_kv.cu:496-500 layout): magic, version, L, H, bytes, digest
-    hb = blobs[:64].cpu().numpy()
-    assert int(hb[:4].view(np.uint32)[0]) == ap.BLOB_MAGIC
-    assert tuple(hb[4:16].view(np.uint32)) == (1, L, H)
-    assert int(hb[24:32].view(np.int64)[0]) == src.store.table_digest
-    dst = Harness(0, page, overflow_records=32)
-    for s_b, d_b in zip(SRC, DST):
-        dst.ref[:, :, d_b] = src.ref[:, :, s_b]
-    offsets = [i * stride for i in range(len(SRC))]
-    assert _import(dst, blobs, offsets, DST) == [0] * len(DST)
+    hdr = blobs[:64].cpu().numpy()
+    assert int(hdr[:4].view(np.uint32)[0]) == ap.BLOB_MAGIC
+    assert tuple(hdr[4:16].view(np.uint32)) == (1, src.L, H)
+    assert int(hdr[24:32].view(np.int64)[0]) == src.store.table_digest
+    # same seed: same calibration, so the destination accepts the digest
+    dst = SimEngine(0, heads=H, page=page, overflow=32)
+    targets = [11, 10, 9, 7, 6][: len(closed)]
+    for s_b, d_b in zip(closed, targets):
+        dst.kv[:, :, d_b] = src.kv[:, :, s_b]
+    offsets = [i * stride for i in range(len(closed))]
+    assert _import(dst, blobs, offsets, targets) == [0] * len(targets)
     torch.cuda.synchronize()
-    assert dst.check_arena(DST) == (1, spills)
-    assert _overflow_used(dst.store, dst.overflow_records) == 1 + spills
-    # re-importing frees the overflow records it replaces
-    assert _import(dst, blobs, offsets, DST) == [0] * len(DST)
-    assert _overflow_used(dst.store, dst.overflow_records) == 1 + spills
-    dst.check_gather({b: T for b in DST})
-    dst.check_decode([[6, 7], [2], [3, 9]], [256, 128, 256])
+    fallbacks, spills = dst.check_records(targets)
+    assert fallbacks == 1 and _overflow_in_use(dst) == fallbacks + spills
+    assert _import(dst, blobs, offsets, targets) == [0] * len(targets)  # frees what it replaces
+    assert _overflow_in_use(dst) == fallbacks + spills
+    dst.check_gather({b: T for b in targets})
 
 
-def test_blob_import_rejects_without_side_effects():
+def test_blob_import_rejects_bad_blobs_untouched():
     import torch
 
     from fragpack_amd.compression import attn_page as ap
 
-    src = Harness(0, _page_bytes())
-    _prefill(src)
-    blobs, _ = _export(src, [8, 9])
+    src = SimEngine(0, noisy={(3, 0, 0, 1)})
+    _serve(src)
+    blobs, _ = _export(src, [3, 4])
     stride = src.store.blob_stride
-    dst = Harness(0, _page_bytes(), overflow_records=1)
+    dst = SimEngine(0, overflow=1)
     before = dst.store.rec_addr.clone(), dst.store.rec_len.clone()
     bad = blobs.clone()
     bad[0] ^= 1  # magic
-    bad[stride + ap.BLOB_FIXED_BYTES] = 8  # a var length that is not a record size
+    bad[stride + ap.BLOB_FIXED_BYTES] = 8  # a length that is no record size
     assert _import(dst, bad, [0, stride], [5, 6]) == [1, 2]
-    other = Harness(1, _page_bytes())  # other calibration: other digest
-    assert _import(other, blobs, [0], [5]) == [1]
+    assert _import(SimEngine(1), blobs, [0], [5]) == [1]  # other tables: other digest
     torch.cuda.synchronize()
-    assert torch.equal(dst.store.rec_addr, before[0])
-    assert torch.equal(dst.store.rec_len, before[1])
-    # block 9's WIDE record takes the only overflow slot; a second copy finds
-    # the pool full in that layer and must release what it took
-    assert _import(dst, blobs, [stride], [9]) == [0]
-    assert _import(dst, blobs, [stride], [10]) == [4]
-    assert _overflow_used(dst.store, 1) == 1
-    torch.cuda.synchronize()
-    assert torch.equal(dst.store.rec_addr[WIDE[1], 10], before[0][WIDE[1], 10])
-
-
-def test_store_errors_surface():
-    """An exhausted overflow pool is reported (StoreError), not silent."""
-    from fragpack_amd.ops.hbm_kv import StoreError
-
-    h = Harness(0, 2 * H * DENSE - 16, overflow_records=2)
-    _prefill(h)
-    import torch
-
-    torch.cuda.synchronize()
-    with pytest.raises(StoreError):
-        h.store.stats()
+    assert torch.equal(dst.store.rec_addr, before[0]) and torch.equal(dst.store.rec_len, before[1])
+    # block 3's incompressible record takes the only overflow slot; a second
+    # copy finds the pool full and must release what it took
+    assert _import(dst, blobs, [0], [9]) == [0]
+    assert _import(dst, blobs, [0], [10]) == [4]
+    assert _overflow_in_use(dst) == 1
+    assert torch.equal(dst.store.rec_addr[0, 10], before[0][0, 10])
