@@ -32,6 +32,9 @@
 #include <algorithm>
 #include <math.h>
 #include <stdint.h>
+#include <stdio.h>
+
+#include <mutex>
 
 #include "../../include/fragpack_hip.h"
 #include "fp_capi_internal.hpp"
@@ -1053,4 +1056,77 @@ extern "C" int fp_fused_decode_append(const void* q, int64_t q_stride, int64_t b
   return decode_launch(p, q, q_stride, batch, kv_heads, group, rec_addr, rec_len, plut, slut, block_table, bt_stride,
                        seq_lens, opart, opart_elems, ml, ml_elems, plan, plan_elems, out, out_stride, units, replan,
                        scale, stream);
+}
+
+// ---------------------------------------------------------------------------
+// fp_fused_decode_noalloc: fp_fused_decode with its split-KV workspace (the
+// partials, their (m, l) pairs and the plan with its merge counters) in a
+// static device array instead of caller buffers, for callers that cannot
+// allocate device memory.  Each device holds its own copy of ``scratch`` for
+// the life of the process; its address is looked up once per device (with
+// that device current) and kept.  Every call launches the planner, which
+// rewrites the plan and zeroes the merge counters, so no state is carried
+// between calls; calls that overlap on one device share the array and race.
+constexpr int64_t kNoAllocBytes = 32LL << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The calling device's copy of ``scratch`` (nullptr with the error set).
+uint8_t* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fp::set_error("fp_fused_decode_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || ptr == nullptr) {
+      fp::set_error("fp_fused_decode_noalloc: hipGetSymbolAddress(scratch) failed");
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
+
+constexpr int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+}  // namespace
+
+extern "C" int64_t fp_fused_decode_noalloc_capacity(void) { return kNoAllocBytes; }
+
+extern "C" int fp_fused_decode_noalloc(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads,
+                                       int64_t group, const int64_t* rec_addr, const int32_t* rec_len,
+                                       const uint32_t* plut, const uint8_t* slut, const int32_t* block_table,
+                                       int64_t bt_stride, const int32_t* seq_lens, void* out, int64_t out_stride,
+                                       int64_t units, double scale, fp_stream_t stream) {
+  FP_CHECK(kv_heads > 0 && units > 0 && units < (1 << 24), "noalloc decode needs kv_heads > 0 and 0 < units < 2^24");
+  const int64_t opart_elems = kv_heads * units * 8 * fp::kDim;
+  const int64_t ml_elems = kv_heads * units * 16;
+  const int64_t plan_elems = fp::ud_offset((int)units) + 8 * units + units * kv_heads;
+  const int64_t ml_off = align256(opart_elems * 4), plan_off = ml_off + align256(ml_elems * 4);
+  const int64_t need = plan_off + plan_elems * 4;
+  if (need > kNoAllocBytes) {
+    char msg[200];
+    snprintf(msg, sizeof msg, "fp_fused_decode_noalloc: workspace of %lld bytes (kv_heads %lld x units %lld) exceeds the "
+             "static scratch of %lld bytes", (long long)need, (long long)kv_heads, (long long)units,
+             (long long)kNoAllocBytes);
+    fp::set_error(msg);
+    return -1;
+  }
+  uint8_t* base = device_scratch();
+  if (base == nullptr) return -1;
+  fp::AttnParams p{};
+  p.nk = p.nv = nullptr;
+  return fp::decode_launch(p, q, q_stride, batch, kv_heads, group, rec_addr, rec_len, plut, slut, block_table,
+                           bt_stride, seq_lens, reinterpret_cast<float*>(base), opart_elems,
+                           reinterpret_cast<float*>(base + ml_off), ml_elems,
+                           reinterpret_cast<int32_t*>(base + plan_off), plan_elems, out, out_stride, units,
+                           /*replan=*/1, scale, stream);
 }

@@ -106,6 +106,26 @@ int fp_fused_decode_append(const void* q, int64_t q_stride, int64_t batch, int64
                            int64_t staging_bytes, const void* scratch, int64_t scratch_bytes,
                            fp_stream_t stream);
 
+/*
+ * fp_fused_decode without caller workspaces, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split-KV partials, (m, l) pairs and plan live in a static device array of
+ * fp_fused_decode_noalloc_capacity() bytes (32 MiB) that each device holds
+ * for the life of the process; a call needing more (about
+ * 4 KiB x kv_heads x units) returns -1 with an error.  Every call launches
+ * the planner (replan 1), which also zeroes the merge counters.  Calls that
+ * overlap on one device share the array and race: serialise them (one
+ * stream).  Arguments as fp_fused_decode minus the workspace and replan.
+ */
+int fp_fused_decode_noalloc(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
+                            const int64_t* rec_addr, const int32_t* rec_len, const uint32_t* plut,
+                            const uint8_t* slut, const int32_t* block_table, int64_t bt_stride,
+                            const int32_t* seq_lens, void* out, int64_t out_stride, int64_t units, double scale,
+                            fp_stream_t stream);
+/* Bytes of the static workspace behind fp_fused_decode_noalloc. */
+int64_t fp_fused_decode_noalloc_capacity(void);
+
 /* Step start: GC, staging claims, close list.  Replaces hbm_prepare
  * (fragpack_ext.cpp:11-17, hbm_kv.cu:669-686). */
 int fp_hbm_prepare(const fp_store_t* s, const int64_t* slot_mapping, int64_t n_tok, const int32_t* live,

@@ -111,7 +111,7 @@ def test_store_rejects_mismatched_tables():
 
 def _declared_symbols():
     text = (ROOT / "include" / "fragpack_hip.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(fp_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(fp_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
