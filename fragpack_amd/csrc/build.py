@@ -15,7 +15,7 @@ import sys
 CSRC = Path(__file__).resolve().parent
 ROOT = CSRC.parent.parent
 OUT = CSRC.parent / "_lib" / "libfragpack_hip.so"
-SOURCES = ["fp_attn.hip", "fp_store.hip", "fp_prefill.hip", "fp_capi.cpp"]
+SOURCES = ["fp_attn.hip", "fp_store.hip", "fp_prefill.hip", "fp_paged.hip", "fp_capi.cpp"]
 ARCH = os.environ.get("FRAGPACK_ARCH", "gfx950")
 
 

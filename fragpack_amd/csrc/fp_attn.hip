@@ -245,36 +245,6 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
                                                  0, 0);
 }
 
-// Split-KV partials are handed between workgroups (possibly on different
-// XCDs, each with its own L2) through per-location coherent accesses:
-// agent-scope relaxed atomic stores and loads (sc1: written through to, and
-// read from, the device coherence point).  A writer waits for its stores to
-// be acknowledged (s_waitcnt) before bumping the group counter, and a reader
-// issues its loads only after seeing the counter complete.  This avoids the
-// whole-L2 writeback / invalidate an agent-scope fence costs on a multi-XCD
-// part once per workgroup.
-// Coherent (sc1) 16- / 8-byte accesses through a buffer resource over a
-// float array of < 2^31 bytes; ``i`` is the float index.
-constexpr int kSc1 = 16;  // cache-policy bit of buffer instructions: sc1
-__device__ __forceinline__ rsrc_t coh_rsrc(const float* base) { return make_rsrc(base, 0x7fffffff); }
-__device__ __forceinline__ void st_coh4(rsrc_t r, int64_t i, float a, float b, float c, float d) {
-  const f32x4 v = {a, b, c, d};
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)(4 * i), 0, kSc1);
-}
-__device__ __forceinline__ void st_coh2(rsrc_t r, int64_t i, float a, float b) {
-  const float2v v = {a, b};
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, (int)(4 * i), 0, kSc1);
-}
-__device__ __forceinline__ float4 ld_coh4(rsrc_t r, int64_t i) {
-  const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(4 * i), 0, kSc1));
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ float2 ld_coh2(rsrc_t r, int64_t i) {
-  const float2v v = __builtin_bit_cast(float2v, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(4 * i), 0, kSc1));
-  return make_float2(v[0], v[1]);
-}
-// Waits until every store this wave issued is acknowledged.
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
 // A operand of MFMA (j, a) from words 2a (w0) and 2a+1 (w1) of a lane's
 // decoded thread: slots (x, f, e) = word 2a + x, dword 2j + f, half e.

@@ -185,6 +185,39 @@ __device__ __forceinline__ uint2 bld8(rsrc_t r, int voff, int soff) {
   return make_uint2(v.x, v.y);
 }
 
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float2vv __attribute__((ext_vector_type(2)));
+// Split-KV partials are handed between workgroups (possibly on different
+// XCDs, each with its own L2) through per-location coherent accesses:
+// agent-scope relaxed atomic stores and loads (sc1: written through to, and
+// read from, the device coherence point).  A writer waits for its stores to
+// be acknowledged (s_waitcnt) before bumping the group counter, and a reader
+// issues its loads only after seeing the counter complete.  This avoids the
+// whole-L2 writeback / invalidate an agent-scope fence costs on a multi-XCD
+// part once per workgroup.
+// Coherent (sc1) 16- / 8-byte accesses through a buffer resource over a
+// float array of < 2^31 bytes; ``i`` is the float index.
+constexpr int kSc1 = 16;  // cache-policy bit of buffer instructions: sc1
+__device__ __forceinline__ rsrc_t coh_rsrc(const float* base) { return make_rsrc(base, 0x7fffffff); }
+__device__ __forceinline__ void st_coh4(rsrc_t r, int64_t i, float a, float b, float c, float d) {
+  const float4v v = {a, b, c, d};
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)(4 * i), 0, kSc1);
+}
+__device__ __forceinline__ void st_coh2(rsrc_t r, int64_t i, float a, float b) {
+  const float2vv v = {a, b};
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, (int)(4 * i), 0, kSc1);
+}
+__device__ __forceinline__ float4 ld_coh4(rsrc_t r, int64_t i) {
+  const float4v v = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(4 * i), 0, kSc1));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float2 ld_coh2(rsrc_t r, int64_t i) {
+  const float2vv v = __builtin_bit_cast(float2vv, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(4 * i), 0, kSc1));
+  return make_float2(v[0], v[1]);
+}
+// Waits until every store this wave issued is acknowledged.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Loads dense data of kernel-order thread 64 * slab + nt (nt < 64) of the
 // record behind ``r``.
 __device__ __forceinline__ void load_slab(rsrc_t r, bool raw, int slab, int nt, SlabBuf& b) {

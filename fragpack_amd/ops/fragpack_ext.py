@@ -120,6 +120,9 @@ class Extension:
             "fp_hbm_import": [sp, _p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p],
             "fp_encode_records": [_p, _i64, _p, _p, _p, _i64, _p, _p, _p],
             "fp_decode_records": [_p, _p, _i64, _p, _p, _p, _p, _i64, _p, _p],
+            "fp_paged_decode": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p,
+                                _i64, _p, _i64, _p, _i64, _f64, _p],
+            "fp_paged_decode_splits": [_i64, _i64, _i64],
             "fp_prefill_attention": [_p, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _f64,
                                      _i32, _p, _i64, _p],
         }
@@ -291,6 +294,34 @@ class Extension:
         self._call("fp_decode_records", _dev(rec_addr, "rec_addr"), _dev(rec_len, "rec_len"), n, _dev(kv, "kv"),
                    _dev(plut, "plut"), _dev(slut, "slut"), _dev(tab_idx, "tab_idx"), slut.numel() // 16,
                    _dev(out, "out"), _stream(out))
+
+    # -- plain BF16 paged decode (the baseline arm; the FA3 call of fragpack_step_bench.py:205-284) --
+    def paged_decode_splits(self, batch: int, kv_heads: int, max_seq_len: int) -> int:
+        return int(self._lib.fp_paged_decode_splits(int(batch), int(kv_heads), int(max_seq_len)))
+
+    def paged_decode(self, q, k_cache, v_cache, block_table, seq_lens, max_seq_len: int, splits: int, opart, ml,
+                     counters, out, scale: float) -> None:
+        B = q.size(0)
+        if B == 0:
+            return
+        _check(q.dtype == torch.bfloat16 and q.dim() == 3 and q.size(2) == 128 and q.stride(2) == 1
+               and q.stride(1) == 128, "q must be BF16 [B, Hq, 128] with contiguous heads")
+        _check(k_cache.dtype == torch.bfloat16 and k_cache.dim() == 4 and k_cache.size(1) == 128
+               and k_cache.size(3) == 128 and k_cache.is_contiguous() and v_cache.shape == k_cache.shape
+               and v_cache.dtype == torch.bfloat16 and v_cache.is_contiguous(),
+               "k / v caches must be contiguous BF16 [blocks, 128, H, 128]")
+        _check(out.shape == q.shape and out.dtype == torch.bfloat16 and out.stride(2) == 1 and out.stride(1) == 128,
+               "out must match q")
+        _check(block_table.dtype == torch.int32 and block_table.stride(1) == 1 and seq_lens.dtype == torch.int32,
+               "block_table int32 [B, pages] with contiguous rows, seq_lens int32 [B]")
+        kvh = k_cache.size(2)
+        group = q.size(1) // kvh
+        _check(group * kvh == q.size(1), "query heads must be a multiple of the KV heads")
+        self._call("fp_paged_decode", _dev(q, "q"), q.stride(0), B, kvh, group, _dev(k_cache, "k_cache"),
+                   _dev(v_cache, "v_cache"), k_cache.size(0), _dev(block_table, "block_table"), block_table.stride(0),
+                   _dev(seq_lens, "seq_lens"), int(max_seq_len), int(splits), _dev(opart, "opart"), opart.numel(),
+                   _dev(ml, "ml"), ml.numel(), _dev(counters, "counters"), counters.numel(), _dev(out, "out"),
+                   out.stride(0), float(scale), _stream(q))
 
     # -- prefill (the FlashAttention call of backend.py:560-575) --
     def prefill_attention(self, q, wk, wv, out, cu_seqlens_q, seqused_k, block_table, max_seqlen_q: int,

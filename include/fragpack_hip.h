@@ -126,6 +126,26 @@ int fp_fused_decode_noalloc(const void* q, int64_t q_stride, int64_t batch, int6
 /* Bytes of the static workspace behind fp_fused_decode_noalloc. */
 int64_t fp_fused_decode_noalloc_capacity(void);
 
+/*
+ * Decode attention over a plain paged BF16 cache: the uncompressed baseline
+ * arm.  Replaces the FA3 call the reference benchmarks against
+ * (benchmarks/fragpack_step_bench.py:205-284, flash_attn_with_kvcache).
+ *   k_cache, v_cache BF16 [num_blocks, 128, kv_heads, 128] (contiguous);
+ *   block_table int32 [batch, bt_stride]; seq_lens int32 [batch], each
+ *   <= max_seq_len.  splits (from fp_paged_decode_splits) workgroups share
+ *   each (sequence, head); with splits > 1 the workspace is opart float
+ *   [batch * kv_heads * splits * 8 * 128], ml float [... * 8 * 2] and
+ *   counters int32 [batch * kv_heads], zero before the first call (every
+ *   completed call leaves them zero).
+ */
+int fp_paged_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
+                    const void* k_cache, const void* v_cache, int64_t num_blocks, const int32_t* block_table,
+                    int64_t bt_stride, const int32_t* seq_lens, int64_t max_seq_len, int64_t splits, float* opart,
+                    int64_t opart_elems, float* ml, int64_t ml_elems, int32_t* counters, int64_t counter_elems,
+                    void* out, int64_t out_stride, double scale, fp_stream_t stream);
+/* Splits per (sequence, head) that fill the current device. */
+int fp_paged_decode_splits(int64_t batch, int64_t kv_heads, int64_t max_seq_len);
+
 /* Step start: GC, staging claims, close list.  Replaces hbm_prepare
  * (fragpack_ext.cpp:11-17, hbm_kv.cu:669-686). */
 int fp_hbm_prepare(const fp_store_t* s, const int64_t* slot_mapping, int64_t n_tok, const int32_t* live,
