@@ -151,6 +151,60 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
                 scale=scale, comp_ratio=comp_ratio, max_err=err.max().item())
 
 
+def paged_bench(torch, args) -> dict:
+    """The plain BF16 paged baseline arm: the same decode step (same shape,
+    same KV distribution, pages in permuted order) through the hand-written
+    BF16 paged decode kernel (fp_paged_decode) over a token-major
+    [blocks, 128, H, 128] cache -- the role FA3 plays in the reference's step
+    benchmark (benchmarks/fragpack_step_bench.py:205-284).  Bytes per step =
+    the K and V pages read (128 x 256 B per page per head each) + Q + out."""
+    from fragpack_amd.ops.paged_attn import paged_decode_attention, paged_splits, paged_workspace
+
+    B, H, G, ctx = args.batch, args.heads, args.group, args.context
+    rng = np.random.default_rng(args.seed + 11)
+    scales = channel_scales(rng, H, 0.02)
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 11)
+    pages = math.ceil(ctx / T)
+    nb = B * pages
+    kv = gen_kv(torch, gen, nb * T, H, torch.from_numpy(scales).float().cuda()).view(2, nb, T, H, D)
+    bt = torch.from_numpy(rng.permutation(nb).astype(np.int32)).cuda().view(B, pages).contiguous()
+    lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    q = torch.randn((B, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    splits = paged_splits(B, H, ctx)
+    ws = paged_workspace(B, H, splits, q.device)
+    scale = D ** -0.5
+
+    def step():
+        paged_decode_attention(q, kv[0], kv[1], bt, lens, ctx, scale, out, ws, splits)
+
+    out.fill_(float("nan"))
+    step()
+    torch.cuda.synchronize()
+    ref = reference_decode(torch, q, kv.view(2, nb * T, H, D), bt.cpu(), lens.cpu().numpy(), H, G, scale)
+    err = (out.float() - ref).abs()
+    valid = bool(torch.isfinite(out.float()).all() and (err <= 2e-2 + 1e-2 * ref.abs()).all())
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream()
+    ms = []
+    for _ in range(2):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1) / args.steps)
+    step_ms = ms[-1]
+    nbytes = 2 * nb * T * H * D * 2 + 2 * B * H * G * D * 2
+    log(f"BF16 paged arm B{B} H{H} G{G} {ctx}: {step_ms * 1e3:.1f} us/step ({nbytes / step_ms / 1e6:.0f} GB/s), "
+        f"splits {splits}, max err {err.max().item():.3e}, valid {valid}")
+    del kv
+    return dict(step_ms=step_ms, bytes=nbytes, valid=valid, splits=splits, max_err=err.max().item())
+
+
 def prefill_bench(torch, args) -> dict:
     """Causal prefill over config 4's prompts: ``--prefill-seqs`` x
     ``--prefill-len`` tokens, 32 query heads over 8 KV heads (GQA 4), on a
@@ -502,13 +556,14 @@ def main() -> None:
     enc_ordered = None if args.no_encode else encode_bench(torch, args, ordered=True)
     pre = None if args.no_prefill else prefill_bench(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(torch, res, args)
+    paged = None if args.no_raw_arm else paged_bench(torch, args)
     raw = None
     if not args.no_raw_arm:
         for k in ("store", "arena"):
             res.pop(k)
         torch.cuda.empty_cache()
         raw = decode_bench(torch, args, raw=True)
-    large = large_raw = None
+    large = large_raw = large_paged = None
     if not args.no_large:
         # config 4's decode sweep shape: B64 x H8 x G4 x 32768 context
         largs = argparse.Namespace(**vars(args))
@@ -527,6 +582,8 @@ def main() -> None:
             large_raw = decode_bench(torch, largs, raw=True)
             for k in ("store", "arena"):
                 large_raw.pop(k)
+            torch.cuda.empty_cache()
+            large_paged = paged_bench(torch, largs)
     layer_steps = []
     if not args.no_layer_step:
         # one layer of a serving decode step: config 1's shape and config 4's
@@ -550,11 +607,14 @@ def main() -> None:
                 for k in ("store", "arena"):
                     r.pop(k)
                 arms.append(r)
+                torch.cuda.empty_cache()
+            pg = paged_bench(torch, sargs)
             sweep.append({"context": ctx, "batch": 64, "kv_heads": 8, "group": 4,
                           "compressed_us_per_step": round(arms[0]["step_ms"] * 1e3, 1),
-                          "bf16_paged_us_per_step": round(arms[1]["step_ms"] * 1e3, 1),
-                          "compressed_step_speedup": round(arms[1]["step_ms"] / arms[0]["step_ms"], 3),
-                          "validated": arms[0]["valid"] and arms[1]["valid"]})
+                          "bf16_paged_us_per_step": round(pg["step_ms"] * 1e3, 1),
+                          "compressed_step_speedup": round(pg["step_ms"] / arms[0]["step_ms"], 3),
+                          "all_raw_records_us_per_step": round(arms[1]["step_ms"] * 1e3, 1),
+                          "validated": arms[0]["valid"] and arms[1]["valid"] and pg["valid"]})
     torch.cuda.empty_cache()
     ceil = None if args.no_ceilings else hbm_ceilings(torch)
     step_s = res["step_ms"] / 1e3
@@ -598,9 +658,16 @@ def main() -> None:
                            "tflops": round(tf, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                            "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "validated": pre["valid"],
                            "sampled_max_abs_err": pre["max_err"]}
-    if raw is not None:
+    if paged is not None:
         line["bf16_paged_arm"] = {
-            "what": "same step over all-raw records (every record 32 KB BF16: the paged BF16 baseline)",
+            "what": "the same step through the plain BF16 paged decode kernel (fp_paged_decode) over a "
+                    "[blocks, 128, H, 128] cache (the reference benchmark's FA3 arm)",
+            "us_per_step": round(paged["step_ms"] * 1e3, 2), "splits": paged["splits"], "validated": paged["valid"],
+            "compressed_step_speedup": round(paged["step_ms"] / res["step_ms"], 3),
+            "hbm_GBps": round(paged["bytes"] / (paged["step_ms"] / 1e3) / 1e9, 1)}
+    if raw is not None:
+        line["all_raw_record_arm"] = {
+            "what": "the FragPack kernel over all-raw records (every record 32 KB BF16 in kernel order)",
             "us_per_step": round(raw["step_ms"] * 1e3, 2), "kernel_us": round(raw["kern_ms"] * 1e3, 2),
             "validated": raw["valid"], "compressed_step_speedup": round(raw["step_ms"] / res["step_ms"], 3),
             "hbm_GBps": round(raw["algo_bytes"] / (raw["kern_ms"] / 1e3) / 1e9, 1)}
@@ -615,8 +682,14 @@ def main() -> None:
             "roofline": {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(la, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(la / HBM_PEAK_GBS, 4),
                          "algo_bytes_per_launch": large["algo_bytes"]}}
-        if large_raw is not None:
+        if large_paged is not None:
             line["decode_large"]["bf16_paged_arm"] = {
+                "us_per_step": round(large_paged["step_ms"] * 1e3, 1), "splits": large_paged["splits"],
+                "validated": large_paged["valid"],
+                "compressed_step_speedup": round(large_paged["step_ms"] / large["step_ms"], 3),
+                "hbm_GBps": round(large_paged["bytes"] / (large_paged["step_ms"] / 1e3) / 1e9, 1)}
+        if large_raw is not None:
+            line["decode_large"]["all_raw_record_arm"] = {
                 "us_per_step": round(large_raw["step_ms"] * 1e3, 1),
                 "kernel_us": round(large_raw["kern_ms"] * 1e3, 1), "validated": large_raw["valid"],
                 "compressed_step_speedup": round(large_raw["step_ms"] / large["step_ms"], 3),
