@@ -681,6 +681,7 @@ def main() -> None:
             "effective_GBps": round(large["eff_bytes"] / lk / 1e9, 1), "compression": round(large["comp_ratio"], 4),
             "roofline": {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(la, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(la / HBM_PEAK_GBS, 4),
+                         "traffic": (profiled_traffic("attn_kernel", "config4") or {}).get("traffic_bytes_per_launch"),
                          "algo_bytes_per_launch": large["algo_bytes"]}}
         if large_paged is not None:
             line["decode_large"]["bf16_paged_arm"] = {
