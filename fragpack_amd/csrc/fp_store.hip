@@ -352,40 +352,100 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
 // (2p, 2p+1) of K (one u32: both scalars are in the same kernel-order word)
 // and of V (two u16: a V pair belongs to two threads) into the raw
 // kernel-order staging record.
-__global__ void __launch_bounds__(kThreads) write_kernel(Store s, const uint16_t* k, const uint16_t* v, int64_t ks0,
-                                                        int64_t ks1, int64_t vs0, int64_t vs1, const int64_t* slots,
-                                                        int n, int layer) {
-  const int item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (item >= n * s.H) return;
+__device__ __forceinline__ void put_k_row(uint8_t* rec, const uint16_t* krow, int off, int p) {
+  const uint32_t val = *reinterpret_cast<const uint32_t*>(krow + 2 * p);
+  // K: token off = 16 tw + 8 j + g, dim 2p = 16 st + 8 f + 2 c
+  const int st = p >> 3, f = (p >> 2) & 1, c = p & 3;
+  const int tw = off >> 4, j = (off >> 3) & 1, g = off & 7;
+  const int t = 32 * tw + 4 * g + c;
+  *reinterpret_cast<uint32_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f)) = val;
+}
+
+__device__ __forceinline__ void put_v_row(uint8_t* rec, const uint16_t* vrow, int off, int p) {
+  const uint32_t val = *reinterpret_cast<const uint32_t*>(vrow + 2 * p);
+  // V: token off = 16 st + 8 f + 2 c + e, dim d = 16 tw + 8 j + g
+  const int st = off >> 4, f = (off >> 3) & 1, c = (off >> 1) & 3, e = off & 1;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int d = 2 * p + q;
+    const int tw = d >> 4, j = (d >> 3) & 1, g = d & 7;
+    const int t = 32 * tw + 4 * g + c;
+    *reinterpret_cast<uint16_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f + e)) = (uint16_t)(val >> (16 * q));
+  }
+}
+
+// The step's new tokens as the write hands them over (element strides).
+struct StepTokens {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t ks0, ks1, vs0, vs1;
+  const int64_t* slots;
+  int n;
+  int enc_grid;  // write + encode in one launch: workgroups [0, enc_grid) encode, the rest write
+};
+
+// (token, head) item ``item`` of the write: K and V rows of token item / H,
+// head item % H, into the staging of the token's block.  With
+// ``skip_closing``, tokens of blocks on the close list are left to the
+// encoders of those blocks (the fused write + encode).
+__device__ __forceinline__ void write_item(const Store& s, const StepTokens& tk, int layer, int item,
+                                           bool skip_closing) {
+  if (item >= tk.n * s.H) return;
   const int tok = item / s.H, h = item % s.H;
-  const int64_t sl = slots[tok];
+  const int64_t sl = tk.slots[tok];
   if (sl < 0) return;
   const int b = (int)(sl >> 7), off = (int)(sl & 127);
+  if (b >= s.NB) return;
   const int w = s.wslot[b];
   if (w < 0) return;
   const int p = threadIdx.x & 63;
-  {
-    const uint32_t val = *reinterpret_cast<const uint32_t*>(k + tok * ks0 + h * ks1 + 2 * p);
-    // K: token off = 16 tw + 8 j + g, dim 2p = 16 st + 8 f + 2 c
-    const int st = p >> 3, f = (p >> 2) & 1, c = p & 3;
-    const int tw = off >> 4, j = (off >> 3) & 1, g = off & 7;
-    const int t = 32 * tw + 4 * g + c;
-    uint8_t* rec = staging_addr(s, w, layer, h);
-    *reinterpret_cast<uint32_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f)) = val;
-  }
-  {
-    const uint32_t val = *reinterpret_cast<const uint32_t*>(v + tok * vs0 + h * vs1 + 2 * p);
-    // V: token off = 16 st + 8 f + 2 c + e, dim d = 16 tw + 8 j + g
-    const int st = off >> 4, f = (off >> 3) & 1, c = (off >> 1) & 3, e = off & 1;
-    uint8_t* rec = staging_addr(s, w, layer, s.H + h);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int d = 2 * p + q;
-      const int tw = d >> 4, j = (d >> 3) & 1, g = d & 7;
-      const int t = 32 * tw + 4 * g + c;
-      *reinterpret_cast<uint16_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f + e)) = (uint16_t)(val >> (16 * q));
+  if (skip_closing) {
+    const int n_closes = s.counters[kCloses];
+    for (int c0 = 0; c0 < n_closes; c0 += 64) {
+      const int c = c0 + p;
+      if (__ballot(c < n_closes && s.close_list[c] == b) != 0) return;
     }
   }
+  put_k_row(staging_addr(s, w, layer, h), tk.k + tok * tk.ks0 + h * tk.ks1, off, p);
+  put_v_row(staging_addr(s, w, layer, s.H + h), tk.v + tok * tk.vs0 + h * tk.vs1, off, p);
+}
+
+__global__ void __launch_bounds__(kThreads) write_kernel(Store s, StepTokens tk, int layer) {
+  write_item(s, tk, layer, blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6), false);
+}
+
+// The fused write + encode's encoder side: before a workgroup reads record
+// ``kvh`` of closing block ``b``, it writes that record's rows of every
+// token of this step in block ``b`` -- and in the block's heir, whose
+// staging the encoder copies -- itself, so no write of another workgroup
+// has to land first.  The write workgroups skip closing blocks; a heir's
+// rows may be written by both sides, with the same bytes.  Whole workgroup;
+// the rows are stored and visible to the workgroup's later loads on return.
+__device__ void write_own_rows(const Store& s, const StepTokens& tk, int layer, int b, int heir, int kvh) {
+  const int tid = threadIdx.x, p = tid & 63, wave = tid >> 6;
+  const bool is_k = kvh < s.H;
+  const int h = is_k ? kvh : kvh - s.H;
+  for (int i0 = 0; i0 < tk.n; i0 += kThreads) {
+    const int i = i0 + tid;
+    const int64_t sl = i < tk.n ? tk.slots[i] : -1;
+    const int blk = sl >= 0 ? (int)(sl >> 7) : -1;
+    uint64_t m = __ballot(blk >= 0 && (blk == b || blk == heir));
+    while (m != 0) {
+      const int bit = __builtin_ctzll(m);
+      m &= m - 1;
+      const int tok = i0 + 64 * wave + bit;
+      const int tb = __shfl(blk, bit, 64), off = (int)(__shfl((int)(sl & 127), bit, 64));
+      const int w = s.wslot[tb];
+      if (w < 0) continue;
+      uint8_t* rec = staging_addr(s, w, layer, kvh);
+      if (is_k)
+        put_k_row(rec, tk.k + tok * tk.ks0 + h * tk.ks1, off, p);
+      else
+        put_v_row(rec, tk.v + tok * tk.vs0 + h * tk.vs1, off, p);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the rows are stored
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------------------
@@ -631,9 +691,9 @@ __device__ __forceinline__ void stage_record(EncStage& st_buf, const uint8_t* sr
 // writes the page fill.
 enum EncMode { kEncClaim = 0, kEncBlockMajor = 1, kEncMeasure = 2, kEncPlaced = 3 };
 
-template <int kMode>
+template <int kMode, bool kWrite>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kEncodeWgPerCu)))
-encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint8_t* rank_of) {
+encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint8_t* rank_of, StepTokens tk) {
   constexpr bool kBlockMajor = kMode == kEncBlockMajor;
   __shared__ EncShared sh;
   __shared__ EncStage stage;
@@ -641,13 +701,20 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   const int per = 2 * s.H;
   const int n_closes = s.counters[kCloses];
   const int n_rec = n_closes * per;
+  if constexpr (kWrite) {
+    // the step's write: workgroups past the encoders, one wave per (token, head)
+    if ((int)blockIdx.x >= tk.enc_grid) {
+      write_item(s, tk, layer, ((int)blockIdx.x - tk.enc_grid) * (kThreads / 64) + (tid >> 6), true);
+      return;
+    }
+  }
   int r = kBlockMajor ? (int)blockIdx.x * per : (int)blockIdx.x;
   if (r >= n_rec) return;
   // Record metadata (block, heir, staging slot) of this workgroup's records
   // in batches of 64 (record r + j grid in lane j), loaded with vector loads
   // one batch ahead: scalar loads would be waited for at every LDS barrier.
   // The stage streams record r + grid while r is encoded.
-  const int g = (int)gridDim.x;
+  const int g = kWrite ? tk.enc_grid : (int)gridDim.x;
   const int lane = tid & 63;
   // the k-th record of this workgroup: its block (close index) and (kv, head)
   auto rec_kvh = [&](int rr) { return kBlockMajor ? rr % per : rr / n_closes; };
@@ -671,6 +738,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   int b = __builtin_amdgcn_readfirstlane(cb);
   int heir = __builtin_amdgcn_readfirstlane(ch);
   uint8_t* src = staging_addr(s, __builtin_amdgcn_readfirstlane(cw), layer, rec_kvh(r));
+  if constexpr (kWrite) write_own_rows(s, tk, layer, b, heir, rec_kvh(r));
   stage_record(stage, src);
   int rank_kvh = -1;
   // counter increments of this workgroup (thread 0), added once at the end:
@@ -715,6 +783,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     const int r1 = next_rec(r);
     if (r1 < n_rec) {
       src1 = staging_addr(s, w1, layer, rec_kvh(r1));
+      if constexpr (kWrite) write_own_rows(s, tk, layer, b1, heir1, rec_kvh(r1));
       stage_record(stage, src1);
     }
     if (nbatch) {  // the next batch becomes current; load the one after
@@ -1192,27 +1261,42 @@ extern "C" int fp_hbm_prepare(const fp_store_t* d, const int64_t* slot_mapping, 
   return 0;
 }
 
+// Checks of a write's arguments; fills ``tk`` (enc_grid 0).
+static int write_args(const fp_store_t* d, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+                      int64_t v_s0, int64_t v_s1, const int64_t* slot_mapping, int64_t n, int64_t layer,
+                      StepTokens& tk, int64_t& write_grid) {
+  FP_CHECK(n > 0 && layer >= 0 && layer < d->num_layers, "bad token count or layer");
+  FP_CHECK(key && value && slot_mapping, "write needs K, V and the slot mapping");
+  FP_CHECK(k_s0 % 2 == 0 && k_s1 % 2 == 0 && v_s0 % 2 == 0 && v_s1 % 2 == 0,
+           "K/V strides must keep dim pairs 4-byte aligned");
+  FP_CHECK(n < (1LL << 30), "too many tokens in one step");
+  tk = StepTokens{static_cast<const uint16_t*>(key), static_cast<const uint16_t*>(value), k_s0, k_s1, v_s0, v_s1,
+                  slot_mapping, (int)n, 0};
+  const int64_t items = n * d->kv_heads;
+  write_grid = (items + kThreads / 64 - 1) / (kThreads / 64);
+  FP_CHECK(write_grid < (1LL << 30), "too many tokens");
+  return 0;
+}
+
 extern "C" int fp_hbm_write(const fp_store_t* d, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
                             int64_t v_s0, int64_t v_s1, const int64_t* slot_mapping, int64_t n, int64_t layer,
                             fp_stream_t stream) {
   if (n == 0) return 0;
   if (check_store(d)) return -1;
-  FP_CHECK(n > 0 && layer >= 0 && layer < d->num_layers, "bad token count or layer");
-  FP_CHECK(k_s0 % 2 == 0 && k_s1 % 2 == 0 && v_s0 % 2 == 0 && v_s1 % 2 == 0,
-           "K/V strides must keep dim pairs 4-byte aligned");
+  StepTokens tk;
+  int64_t grid = 0;
+  if (write_args(d, key, k_s0, k_s1, value, v_s0, v_s1, slot_mapping, n, layer, tk, grid)) return -1;
   const Store s = make_store(d);
-  const int64_t items = n * d->kv_heads;
-  const int64_t grid = (items + kThreads / 64 - 1) / (kThreads / 64);
-  FP_CHECK(grid < (1LL << 31), "too many tokens");
-  hipLaunchKernelGGL(write_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s,
-                     static_cast<const uint16_t*>(key), static_cast<const uint16_t*>(value), k_s0, k_s1, v_s0, v_s1,
-                     slot_mapping, (int)n, (int)layer);
+  hipLaunchKernelGGL(write_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, tk, (int)layer);
   FP_LAUNCH_CHECK();
   return 0;
 }
 
+// The encode launches; with ``tk`` (non-null) the first one also performs
+// the step's write (write_grid workgroups appended to its grid).
 static int encode_launch(const fp_store_t* d, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
-                         int64_t arena, int64_t page_bytes, int64_t max_close, bool ordered, fp_stream_t stream) {
+                         int64_t arena, int64_t page_bytes, int64_t max_close, bool ordered, fp_stream_t stream,
+                         StepTokens* tk = nullptr, int64_t write_grid = 0) {
   if (max_close == 0) return 0;
   if (check_store(d)) return -1;
   FP_CHECK(max_close > 0 && max_close <= d->list_cap, "close list too small");
@@ -1232,22 +1316,32 @@ static int encode_launch(const fp_store_t* d, const uint8_t* rank_of, int64_t ra
   }
   const int64_t records = max_close * 2 * d->kv_heads;
   const int64_t slots = (int64_t)cus * kEncodeWgPerCu;
-  const int64_t grid = std::min<int64_t>(records, slots);
   uint8_t* arena_p = reinterpret_cast<uint8_t*>(arena);
+  // the first launch's grid: its encoders, plus the write's workgroups when fused
+  StepTokens none{nullptr, nullptr, 0, 0, 0, 0, nullptr, 0, 0};
+  auto launch_first = [&](auto kernel_w, auto kernel, int64_t enc_grid) {
+    if (tk) {
+      tk->enc_grid = (int)enc_grid;
+      hipLaunchKernelGGL(kernel_w, dim3((unsigned)(enc_grid + write_grid)), dim3(kThreads), 0, stream, s,
+                         (int)layer, arena_p, page_bytes, rank_of, *tk);
+    } else {
+      hipLaunchKernelGGL(kernel, dim3((unsigned)enc_grid), dim3(kThreads), 0, stream, s, (int)layer, arena_p,
+                         page_bytes, rank_of, none);
+    }
+  };
+  const int64_t grid = std::min<int64_t>(records, slots);
   if (!ordered) {
-    hipLaunchKernelGGL(encode_kernel<kEncClaim>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
-                       arena_p, page_bytes, rank_of);
+    launch_first(encode_kernel<kEncClaim, true>, encode_kernel<kEncClaim, false>, grid);
   } else if (2 * ((records + slots - 1) / slots) < 2 * d->kv_heads) {
     // few blocks: two parallel passes (each record read twice) finish
     // before one workgroup per block has walked its 2H records
-    hipLaunchKernelGGL(encode_kernel<kEncMeasure>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
-                       arena_p, page_bytes, rank_of);
+    launch_first(encode_kernel<kEncMeasure, true>, encode_kernel<kEncMeasure, false>, grid);
     FP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(encode_kernel<kEncPlaced>, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, (int)layer,
-                       arena_p, page_bytes, rank_of);
+    hipLaunchKernelGGL((encode_kernel<kEncPlaced, false>), dim3((unsigned)grid), dim3(kThreads), 0, stream, s,
+                       (int)layer, arena_p, page_bytes, rank_of, none);
   } else {
-    hipLaunchKernelGGL(encode_kernel<kEncBlockMajor>, dim3((unsigned)std::min<int64_t>(max_close, slots)),
-                       dim3(kThreads), 0, stream, s, (int)layer, arena_p, page_bytes, rank_of);
+    launch_first(encode_kernel<kEncBlockMajor, true>, encode_kernel<kEncBlockMajor, false>,
+                 std::min<int64_t>(max_close, slots));
   }
   FP_LAUNCH_CHECK();
   return 0;
@@ -1262,6 +1356,21 @@ extern "C" int fp_hbm_encode_ordered(const fp_store_t* d, const uint8_t* rank_of
                                      int64_t layer, int64_t arena, int64_t page_bytes, int64_t max_close,
                                      fp_stream_t stream) {
   return encode_launch(d, rank_of, rank_of_elems, layer, arena, page_bytes, max_close, true, stream);
+}
+
+extern "C" int fp_hbm_write_encode(const fp_store_t* d, const void* key, int64_t k_s0, int64_t k_s1,
+                                   const void* value, int64_t v_s0, int64_t v_s1, const int64_t* slot_mapping,
+                                   int64_t n, int64_t layer, const uint8_t* rank_of, int64_t rank_of_elems,
+                                   int64_t arena, int64_t page_bytes, int64_t max_close, int ordered,
+                                   fp_stream_t stream) {
+  if (n == 0) return encode_launch(d, rank_of, rank_of_elems, layer, arena, page_bytes, max_close, ordered != 0, stream);
+  if (max_close == 0) return fp_hbm_write(d, key, k_s0, k_s1, value, v_s0, v_s1, slot_mapping, n, layer, stream);
+  if (check_store(d)) return -1;
+  StepTokens tk;
+  int64_t write_grid = 0;
+  if (write_args(d, key, k_s0, k_s1, value, v_s0, v_s1, slot_mapping, n, layer, tk, write_grid)) return -1;
+  return encode_launch(d, rank_of, rank_of_elems, layer, arena, page_bytes, max_close, ordered != 0, stream, &tk,
+                       write_grid);
 }
 
 extern "C" int fp_hbm_commit(const fp_store_t* d, fp_stream_t stream) {

@@ -114,6 +114,8 @@ class Extension:
             "fp_hbm_write": [sp, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p],
             "fp_hbm_encode": [sp, _p, _i64, _i64, _i64, _i64, _i64, _p],
             "fp_hbm_encode_ordered": [sp, _p, _i64, _i64, _i64, _i64, _i64, _p],
+            "fp_hbm_write_encode": [sp, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64,
+                                    _i32, _p],
             "fp_hbm_commit": [sp, _p],
             "fp_hbm_gather": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _p],
             "fp_hbm_export": [_p, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p],
@@ -222,6 +224,31 @@ class Extension:
         _check(int(page_bytes) % 16 == 0 and int(page_bytes) < (1 << 31), "bad arena page size")
         self._call("fp_hbm_encode_ordered" if ordered else "fp_hbm_encode", ctypes.byref(d), _dev(rank_of, "rank_of"),
                    rank_of.numel(), int(layer), int(arena), int(page_bytes), int(max_close), _stream(rank_of))
+
+    def hbm_write_encode(self, *args, ordered: bool = False) -> None:
+        """hbm_write then hbm_encode of one layer in one launch
+        (fp_hbm_write_encode); same arguments as the two calls."""
+        state, (key, value, slot_mapping, rank_of, layer, arena, page_bytes, max_close) = args[:13], args[13:]
+        n = key.size(0)
+        if int(max_close) == 0:
+            self.hbm_write(*state, key, value, slot_mapping, layer)
+            return
+        if n == 0:
+            self.hbm_encode(*state, rank_of, layer, arena, page_bytes, max_close, ordered=ordered)
+            return
+        _check(key.stride(2) == 1 and value.stride(2) == 1, "head dim must be contiguous")
+        _check(key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16, "K / V must be BF16")
+        _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() >= n, "slot_mapping must be int64 [N]")
+        d = _store_desc(state)
+        _check(key.size(1) == d.kv_heads and key.size(2) == 128 and value.shape == key.shape,
+               "K / V must be [N, H, 128]")
+        _check(2 * int(max_close) <= state[6].numel(), "close list too small")
+        _check(rank_of.numel() == d.num_layers * 2 * d.kv_heads * 256, "rank_of must hold every layer")
+        _check(int(page_bytes) % 16 == 0 and int(page_bytes) < (1 << 31), "bad arena page size")
+        self._call("fp_hbm_write_encode", ctypes.byref(d), _dev(key, "key"), key.stride(0), key.stride(1),
+                   _dev(value, "value"), value.stride(0), value.stride(1), _dev(slot_mapping, "slot_mapping"), n,
+                   int(layer), _dev(rank_of, "rank_of"), rank_of.numel(), int(arena), int(page_bytes),
+                   int(max_close), int(bool(ordered)), _stream(key))
 
     def hbm_commit(self, *state) -> None:
         d = _store_desc(state)

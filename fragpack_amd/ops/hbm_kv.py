@@ -304,6 +304,18 @@ class HbmKvStore:
         extension().hbm_encode(*self._state, self.tables.rank_of, layer, self.arena_base[layer],
                                self.arena_stride[layer], max_close, ordered=ordered)
 
+    def write_encode(self, layer: int, key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor,
+                     max_close: int, ordered: bool = False) -> None:
+        """``write`` then ``encode`` of one layer in one launch (the decode-step
+        fusion; fragpack_step_bench.py:472-610 times the two separately).
+
+        Results equal the two calls'.  The encoders of closing blocks write
+        those blocks' new rows themselves, scanning the whole slot mapping per
+        record: meant for steps of few tokens (decode steps).
+        """
+        extension().hbm_write_encode(*self._state, key, value, slot_mapping, self.tables.rank_of, layer,
+                                     self.arena_base[layer], self.arena_stride[layer], max_close, ordered=ordered)
+
     def commit(self) -> None:
         """After the last layer: release or hand over the closed blocks' staging."""
         extension().hbm_commit(*self._state)

@@ -175,6 +175,20 @@ int fp_hbm_encode(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_e
 int fp_hbm_encode_ordered(const fp_store_t* s, const uint8_t* rank_of, int64_t rank_of_elems, int64_t layer,
                           int64_t arena, int64_t page_bytes, int64_t max_close, fp_stream_t stream);
 
+/* fp_hbm_write followed by fp_hbm_encode (ordered = 0) or
+ * fp_hbm_encode_ordered (ordered = 1) of the same layer, in one launch: the
+ * decode-step fusion the reference's step benchmark measures as separate
+ * launches (fragpack_step_bench.py:472-610, write hbm_kv.cu:223-255 then
+ * encode :262-429).  The workgroups that encode a closing block's records
+ * write that block's (and its heir's) new rows themselves before reading
+ * them; the others write every token of the other blocks.  Same results as
+ * the two calls.  Each closing record's encoder scans the whole slot
+ * mapping, so this suits steps of few tokens (decode steps). */
+int fp_hbm_write_encode(const fp_store_t* s, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+                        int64_t v_s0, int64_t v_s1, const int64_t* slot_mapping, int64_t n, int64_t layer,
+                        const uint8_t* rank_of, int64_t rank_of_elems, int64_t arena, int64_t page_bytes,
+                        int64_t max_close, int ordered, fp_stream_t stream);
+
 /* Release closed blocks' staging.  Replaces hbm_commit
  * (fragpack_ext.cpp:35-39, hbm_kv.cu:725-734). */
 int fp_hbm_commit(const fp_store_t* s, fp_stream_t stream);

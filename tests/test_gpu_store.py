@@ -42,9 +42,12 @@ class SimEngine:
     """A serving engine in miniature: requests own block lists taken from a
     pool (lowest id first); each step schedules some tokens per request and
     runs prepare -> (write, encode) per layer -> commit on the GPU store and
-    on the store model, keeping the written KV on the host."""
+    on the store model, keeping the written KV on the host.  ``fused``: each
+    layer's write and encode go through the one-launch write_encode;
+    ``ordered``: records are placed in (kv, head) order."""
 
-    def __init__(self, seed, layers=2, heads=2, blocks=12, page=None, staging=3, overflow=16, noisy=()):
+    def __init__(self, seed, layers=2, heads=2, blocks=12, page=None, staging=3, overflow=16, noisy=(),
+                 fused=False, ordered=False):
         import torch
 
         from fragpack_amd.compression.attn_tables import calibrate, device_tables
@@ -69,6 +72,7 @@ class SimEngine:
         self.noisy = set(noisy)  # (block, layer, kv, head) written with values too spread to code
         self.filled: dict[int, int] = {}
         self.heirs_seen = 0
+        self.fused, self.ordered = fused, ordered
 
     def _take(self, n):
         got = sorted(self.pool)[:n]
@@ -122,8 +126,12 @@ class SimEngine:
             qkv = torch.empty(n, 3 * self.H, D, dtype=torch.bfloat16, device="cuda")
             qkv[:, self.H : 2 * self.H] = _dev_bits(kv[0])
             qkv[:, 2 * self.H :] = _dev_bits(kv[1])
-            self.store.write(layer, qkv[:, self.H : 2 * self.H], qkv[:, 2 * self.H :], slot_t)
-            self.store.encode(layer, closes)
+            key, value = qkv[:, self.H : 2 * self.H], qkv[:, 2 * self.H :]
+            if self.fused:
+                self.store.write_encode(layer, key, value, slot_t, closes, ordered=self.ordered)
+            else:
+                self.store.write(layer, key, value, slot_t)
+                self.store.encode(layer, closes, ordered=self.ordered)
         self.store.commit()
         self.model.commit()
         self.check_bookkeeping(claims=False)
@@ -246,8 +254,9 @@ def _serve(eng):
     eng.step([("a", 1), ("b", 1), ("d", 1)])
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("tight", [False, True])
-def test_serving_steps_match_model_and_oracle(tight):
+def test_serving_steps_match_model_and_oracle(tight, fused):
     import torch
 
     from fragpack_amd.ops.hbm_kv import page_bytes
@@ -255,7 +264,7 @@ def test_serving_steps_match_model_and_oracle(tight):
     H = 2
     # a tight page holds 3 of a block-layer's 4 records: one spills per block-layer
     page = 2 * H * DENSE - 16 if tight else page_bytes(H)
-    eng = SimEngine(0, heads=H, page=page, noisy={(3, 0, 0, 1)})
+    eng = SimEngine(0, heads=H, page=page, noisy={(3, 0, 0, 1)}, fused=fused)
     _serve(eng)
     torch.cuda.synchronize()
     closed = [b for b, n in eng.filled.items() if n == T]
@@ -271,13 +280,14 @@ def test_serving_steps_match_model_and_oracle(tight):
         eng.check_decode(["a", "b", "d"], group)
 
 
-def test_closing_chunk_hands_its_slot_to_the_new_tail():
+@pytest.mark.parametrize("fused", [False, True])
+def test_closing_chunk_hands_its_slot_to_the_new_tail(fused):
     """With every persistent slot held, a chunk that fills a request's open
     block and opens the next one stages the new tail as an heir, which takes
     the closing block's slot at commit (hbm_kv.py:24-29)."""
     import torch
 
-    eng = SimEngine(1, staging=2)
+    eng = SimEngine(1, staging=2, fused=fused)
     eng.step([("a", 200), ("b", 200)])
     eng.step([("a", 100), ("b", 100)])  # each closes block 1 and opens block 2
     assert eng.heirs_seen == 2
@@ -295,17 +305,65 @@ def test_closing_chunk_hands_its_slot_to_the_new_tail():
     eng.check_decode(["a", "b"], 8)
 
 
-def test_staging_and_overflow_exhaustion_surface():
+@pytest.mark.parametrize("fused", [False, True])
+def test_staging_and_overflow_exhaustion_surface(fused):
     from fragpack_amd.ops.hbm_kv import StoreError
 
-    eng = SimEngine(3, staging=1)
+    eng = SimEngine(3, staging=1, fused=fused)
     eng.step([("a", 10), ("b", 10)])  # two open blocks, one slot
     with pytest.raises(StoreError, match="staging"):
         eng.store.stats()
-    eng = SimEngine(3, heads=2, page=2 * 2 * DENSE - 16, overflow=2)
+    eng = SimEngine(3, heads=2, page=2 * 2 * DENSE - 16, overflow=2, fused=fused)
     eng.step([("a", 384)])  # 3 closed blocks x 2 layers: 6 spills, 2 slots
     with pytest.raises(StoreError, match="overflow"):
         eng.store.stats()
+
+
+def _placed(eng):
+    """Per layer: (rec_len, record offsets within the arena (-1 elsewhere),
+    the arena bytes of the closed blocks' pages up to their fill)."""
+    closed = sorted(b for b, n in eng.filled.items() if n == T)
+    addr = eng.store.rec_addr.cpu().numpy()
+    out = []
+    for layer in range(eng.L):
+        base, size = eng.caches[layer].data_ptr(), eng.caches[layer].numel()
+        a = addr[layer]
+        off = np.where((a >= base) & (a < base + size), a - base, -1)
+        arena = eng.caches[layer].cpu().numpy()
+        fill = eng.store.fill[layer].cpu().numpy()
+        pages = [arena[b, : fill[b]].tobytes() for b in closed]
+        out.append((eng.store.rec_len[layer].cpu().numpy(), off, pages))
+    return out
+
+
+def test_fused_write_encode_places_records_like_the_two_launches():
+    """Ordered placement depends only on the records, so the one-launch
+    write + encode must leave the same tables and arena bytes as write then
+    encode, step for step -- decode steps (one token per block, some
+    closing), a closing chunk with an heir, and mid-block steps."""
+    import torch
+
+    engines = [SimEngine(5, staging=2, ordered=True, fused=f) for f in (False, True)]
+    # chunks closing a block and opening one with both staging slots held
+    # (heirs), then decode steps, two of which close a block each
+    sched = [[("a", 200), ("b", 200)], [("a", 100), ("b", 100)], [("a", 1), ("b", 1)], [("a", 82), ("b", 81)],
+             [("a", 1), ("b", 1)], [("a", 1), ("b", 1)], [("a", 1), ("b", 1)]]
+    for st in sched:
+        for eng in engines:
+            eng.step(st)
+        torch.cuda.synchronize()
+        got = [_placed(eng) for eng in engines]
+        for (l0, o0, p0), (l1, o1, p1) in zip(*got):
+            np.testing.assert_array_equal(l0, l1)
+            np.testing.assert_array_equal(o0, o1)
+            assert p0 == p1
+        s0, s1 = (eng.store.stats() for eng in engines)
+        assert s0 == s1
+    assert engines[1].heirs_seen > 0
+    for eng in engines:
+        closed = sorted(b for b, n in eng.filled.items() if n == T)
+        eng.check_records(closed)
+        eng.check_gather()
 
 
 # ---------------------------------------------------------------- block blobs
