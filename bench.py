@@ -347,8 +347,10 @@ def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int
     between them, enqueued behind a spinning kernel so that the events see
     the GPU's time (kernels and launch gaps) rather than the host's; the
     step's prepare (once per step, all layers) is timed the same way just
-    before it.  Validated: the encode counter moves by 2 H B (close) or 0,
-    and the last blocks gather back bit-exact."""
+    before it.  The same step is also timed fused: write + encode in one
+    launch (fp_hbm_write_encode), then attention.  Validated (both orders):
+    the encode counter moves by 2 H B (close) or 0, the last blocks gather
+    back bit-exact and the attention output is finite."""
     import statistics
 
     from fragpack_amd.compression.attn_tables import device_tables
@@ -397,39 +399,55 @@ def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int
     want_k = torch.cat((seed[0].view(B, offset, H, D), step_kv[0].view(B, 1, H, D)), dim=1)
     want_v = torch.cat((seed[1].view(B, offset, H, D), step_kv[1].view(B, 1, H, D)), dim=1)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
-    samples = {"prepare": [], "write": [], "attention": [], "encode": [], "layer": []}
-    valid = True
-    for it in range(rounds + 3):
-        store.prepare(seed_slots, seed_slots.numel(), no_live)
-        store.write(0, seed[0], seed[1], seed_slots)
-        store.commit()
-        torch.cuda.synchronize()
-        before = int(store.counters[7].item())
-        # the GPU spins while the operations are enqueued, so the events time
-        # the GPU's work and launch gaps, not the host's enqueue
-        torch.cuda._sleep(2_000_000)
-        ev[4].record()
-        store.prepare(step_slots, B, live)
-        ev[0].record()
-        store.write(0, step_kv[0], step_kv[1], step_slots)
-        ev[1].record()
-        decode_attention(q, tabs, bt, lens, D ** -0.5, units, out, ws, True)
-        ev[2].record()
-        store.encode(0, B, ordered=ordered)
-        ev[3].record()
-        ev[3].synchronize()
-        store.commit()
-        encoded = int(store.counters[7].item()) - before
-        store.gather(0, last.to(torch.int32), wk, wv)
-        ok = (encoded == (2 * H * B if close else 0)
-              and torch.equal(wk[:, : offset + 1].view(torch.int16), want_k.view(torch.int16))
-              and torch.equal(wv[:, : offset + 1].view(torch.int16), want_v.view(torch.int16))
-              and bool(torch.isfinite(out.float()).all()))
-        valid = valid and ok
-        if it >= 3:
-            for k, (a, b) in (("prepare", (4, 0)), ("write", (0, 1)), ("attention", (1, 2)), ("encode", (2, 3)),
-                              ("layer", (0, 3))):
-                samples[k].append(ev[a].elapsed_time(ev[b]) * 1e3)
+
+    def eager(fused: bool):
+        """Timed samples of the step; ``fused``: write + encode in one launch
+        (fp_hbm_write_encode), then attention."""
+        keys = (("prepare", (4, 0)), ("write_encode" if fused else "write", (0, 1)), ("attention", (1, 2)),
+                ("encode", (2, 3)), ("layer", (0, 3)))
+        samples = {k: [] for k, _ in keys if not (fused and k == "encode")}
+        ok_all = True
+        for it in range(rounds + 3):
+            store.prepare(seed_slots, seed_slots.numel(), no_live)
+            store.write(0, seed[0], seed[1], seed_slots)
+            store.commit()
+            torch.cuda.synchronize()
+            before = int(store.counters[7].item())
+            out.fill_(float("nan"))
+            # the GPU spins while the operations are enqueued, so the events
+            # time the GPU's work and launch gaps, not the host's enqueue
+            torch.cuda._sleep(2_000_000)
+            ev[4].record()
+            store.prepare(step_slots, B, live)
+            ev[0].record()
+            if fused:
+                store.write_encode(0, step_kv[0], step_kv[1], step_slots, B, ordered=ordered)
+            else:
+                store.write(0, step_kv[0], step_kv[1], step_slots)
+            ev[1].record()
+            decode_attention(q, tabs, bt, lens, D ** -0.5, units, out, ws, True)
+            ev[2].record()
+            if not fused:
+                store.encode(0, B, ordered=ordered)
+            ev[3].record()
+            ev[3].synchronize()
+            store.commit()
+            encoded = int(store.counters[7].item()) - before
+            store.gather(0, last.to(torch.int32), wk, wv)
+            ok = (encoded == (2 * H * B if close else 0)
+                  and torch.equal(wk[:, : offset + 1].view(torch.int16), want_k.view(torch.int16))
+                  and torch.equal(wv[:, : offset + 1].view(torch.int16), want_v.view(torch.int16))
+                  and bool(torch.isfinite(out.float()).all()))
+            ok_all = ok_all and ok
+            if it >= 3:
+                for k, (x, y) in keys:
+                    if k in samples:
+                        samples[k].append(ev[x].elapsed_time(ev[y]) * 1e3)
+        return samples, ok_all
+
+    samples, valid = eager(False)
+    fused_samples, fused_valid = eager(True)
+    valid = valid and fused_valid
     # The layer's three launches captured once into a HIP graph and replayed
     # (the step's prepare, the seeding and commit stay outside the graph, as
     # in the reference benchmark's graph mode): the launch gaps between them
@@ -472,11 +490,13 @@ def layer_step_bench(torch, args, batch: int, heads: int, group: int, pages: int
             graph_samples.append(ev[0].elapsed_time(ev[3]) * 1e3)
     res = {f"us_{k}": round(statistics.median(v), 1) for k, v in samples.items()}
     res["us_layer_graph"] = round(statistics.median(graph_samples), 1)
+    res["fused"] = {f"us_{k}": round(statistics.median(v), 1) for k, v in fused_samples.items() if k != "prepare"}
     res.update({"batch": B, "kv_heads": H, "group": G, "context_after_step": int(lens[0].item()),
                 "case": ("close_block" if close else "mid_block") + (" (ordered encode)" if ordered else ""),
                 "validated": valid})
     log(f"layer step B{B} H{H} {res['case']}: prepare {res['us_prepare']} us (once per step), write {res['us_write']} us, attention {res['us_attention']} us, "
-        f"encode {res['us_encode']} us, layer {res['us_layer']} us (graph replay {res['us_layer_graph']} us), "
+        f"encode {res['us_encode']} us, layer {res['us_layer']} us (graph replay {res['us_layer_graph']} us); "
+        f"fused write+encode {res['fused']['us_write_encode']} us, then attention: layer {res['fused']['us_layer']} us; "
         f"valid {valid}")
     return res
 

@@ -402,9 +402,17 @@ class FragPackRunner:
         )
 
 
+# Steps of at most this many tokens write and encode each layer in one
+# launch (fp_hbm_write_encode): each closing record's encoder scans the slot
+# mapping, which stays cheap for decode-sized steps.
+FUSED_STEP_TOKENS = 512
+
+
 def layer_forward(md: FragPackMetadata, li: int, query, key, value, output, scale: float):
     """Write one layer's new KV, attend, encode the blocks closed this step,
-    and commit after the last layer (backend.py:537-578).
+    and commit after the last layer (backend.py:537-578); steps of up to
+    ``FUSED_STEP_TOKENS`` tokens write and encode in one launch before
+    attending.
 
     Args:
         md: The step's metadata; None in an engine's profiling run (the
@@ -424,7 +432,14 @@ def layer_forward(md: FragPackMetadata, li: int, query, key, value, output, scal
         return output.zero_()
     store = md.store
     n = md.num_tokens
-    store.write(li, key[:n], value[:n], md.slot_mapping[:n])
+    # A step of few tokens writes and encodes in one launch, before attention
+    # rather than after it: the blocks it closes are then read back from
+    # their coded records, which hold the same bits.
+    fused = n <= FUSED_STEP_TOKENS
+    if fused:
+        store.write_encode(li, key[:n], value[:n], md.slot_mapping[:n], md.max_close)
+    else:
+        store.write(li, key[:n], value[:n], md.slot_mapping[:n])
     nd = md.num_decodes
     if nd:
         decode_attention(query[:nd], md.layer_tables[li], md.decode_block_table, md.decode_seq_lens, scale,
@@ -435,7 +450,8 @@ def layer_forward(md: FragPackMetadata, li: int, query, key, value, output, scal
                                cu_seqlens_q=g.cu_seqlens_q, max_seqlen_q=g.max_seqlen_q, seqused_k=g.seqused_k,
                                max_seqlen_k=g.max_seqlen_k, softmax_scale=scale, causal=True,
                                block_table=g.block_table)
-    store.encode(li, md.max_close)
+    if not fused:
+        store.encode(li, md.max_close)
     if li == md.last_layer:
         store.commit()
     return output
