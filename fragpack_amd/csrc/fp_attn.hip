@@ -50,7 +50,8 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 4;     // wavefronts per workgroup = slabs per record
 constexpr int kAttnPerCu = 3;  // resident workgroups per CU (kWaves = SIMDs per CU; VGPR budget 512 / 3)
 constexpr float kLazyMax = 8.f;    // log2 headroom of the speculative softmax reference
-constexpr int kTileBytes = 8 * 4 * 4 * 16;  // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
+constexpr int kTileRow = 4 * 4 * 16 + 16;   // one head's row of a fragment tile, padded by a chunk
+constexpr int kTileBytes = 8 * kTileRow;    // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
 
 struct AttnParams {
   const uint16_t* q;
@@ -366,9 +367,14 @@ __device__ __forceinline__ int natural_prefix(int cnt, NatPerm np) {
 }
 
 // Fragment tile [head 8][a 4][c 4] x 16 B: lane (c, n) reads its 8 BF16 of
-// k-chunk a at ((n * 4 + a) * 4 + c) * 16.  Used for Q (dims) and P (tokens).
+// k-chunk a from chunk (a * 4 + c) of head row n & 7.  Used for Q (dims) and
+// P (tokens).  Head rows are kTileRow = 272 B apart, one LDS bank row (256 B)
+// plus one chunk, so the eight heads' chunks of one (a, c), which lanes read
+// together, start four banks apart instead of all in the same four banks;
+// the k-chunk stays an immediate offset (a * 64).
+__device__ __forceinline__ int tile_chunk(int n, int a, int c) { return (n & 7) * kTileRow + (a * 4 + c) * 16; }
 __device__ __forceinline__ uint4 tile_frag(const uint8_t* tile, int n, int a, int c) {
-  return *reinterpret_cast<const uint4*>(tile + (((n & 7) * 4 + a) * 4 + c) * 16);
+  return *reinterpret_cast<const uint4*>(tile + tile_chunk(n, a, c));
 }
 
 // Decodes this lane's kernel-order thread ``nt`` of the wave's slab ``w`` of
@@ -705,7 +711,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int j = 4 * (L & 15) + t;
-          const int frag = ((row * 4 + (j >> 4)) * 4 + (j & 3)) * 16, x = (j >> 3) & 1, f = (j >> 2) & 1;
+          const int frag = tile_chunk(row, j >> 4, j & 3), x = (j >> 3) & 1, f = (j >> 2) & 1;
           // lanes L and L ^ 1 hold f = 0 and f = 1 of the same (a, c, x):
           // each writes the dword of e = its own f
           const uint32_t o = __shfl_xor(v[t], 1, 64);
@@ -796,12 +802,13 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         // at slot 4x + 2e + f (f = j, e = r & 1): the even-odd order coded
         // words decode in (a raw V record permutes the fragments)
         if (hh == 0) {
-          uint8_t* base = sh.pt + ((n * 4 + w) * 4 + 2 * (c & 1)) * 16 + 8 * (c >> 1);
+          uint8_t* c0 = sh.pt + tile_chunk(n, w, 2 * (c & 1)) + 8 * (c >> 1);
+          uint8_t* c1 = sh.pt + tile_chunk(n, w, 2 * (c & 1) + 1) + 8 * (c >> 1);
           auto pk = pack_bf16x2;
-          *reinterpret_cast<uint32_t*>(base) = pk(e0[0], e1[0]);
-          *reinterpret_cast<uint32_t*>(base + 4) = pk(e0[1], e1[1]);
-          *reinterpret_cast<uint32_t*>(base + 16) = pk(e0[2], e1[2]);
-          *reinterpret_cast<uint32_t*>(base + 20) = pk(e0[3], e1[3]);
+          *reinterpret_cast<uint32_t*>(c0) = pk(e0[0], e1[0]);
+          *reinterpret_cast<uint32_t*>(c0 + 4) = pk(e0[1], e1[1]);
+          *reinterpret_cast<uint32_t*>(c1) = pk(e0[2], e1[2]);
+          *reinterpret_cast<uint32_t*>(c1 + 4) = pk(e0[3], e1[3]);
         }
       };
       if (spec) softmax_tile(m_run);
