@@ -34,7 +34,8 @@ enum : int {
   kHeirs = 9,
   kDonors = 10,
 };
-enum : int { kTagLive = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
+// tags rows: [0] prepare's list of late closing claims (<= NB entries), [1..3] per-block step stamps
+enum : int { kLateList = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
 
 constexpr int kThreads = 256;
 constexpr int kEncodeWgPerCu = 4;  // resident encode workgroups per CU (LDS: 32 KB stage + 6 KB each)
@@ -164,7 +165,8 @@ __device__ __forceinline__ void ovf_free(const Store& s, int64_t addr) {
 // transient scratch at close_list[cap ..).
 constexpr int kPrepThreads = 1024;
 constexpr int kPrepWaves = kPrepThreads / 64;
-constexpr int kCompactPer = 4;
+constexpr int kCompactPer = 8;
+constexpr int kScanPer = 8;   // slot-mapping entries per thread and round of prepare's first pass
 constexpr int kLiveWords = 8192;  // persistent-slot liveness bitmap: up to 262144 slots
 
 struct PrepShared {
@@ -172,20 +174,26 @@ struct PrepShared {
   int wcnt[kPrepWaves];
 };
 
-// Stream compaction of items [0, n): ``pick(i)`` returns a payload >= 0 to
-// keep item i (or < 0), ``emit(i, rank, payload)`` receives each kept item's
-// rank in input order.  Called by the whole workgroup; returns the count,
-// with every emit's stores done before it returns.
-template <typename Pick, typename Emit>
-__device__ int wg_compact(int n, PrepShared& sh, Pick pick, Emit emit) {
+// Stream compaction of items [0, n): ``load(i)`` fetches what item i's
+// decision needs (a plain load, issued for all of a thread's items before
+// any is decided, so they are in flight together), ``pick(i, v)`` returns a
+// payload >= 0 to keep item i (or < 0), ``emit(i, rank, payload)`` receives
+// each kept item's rank in input order.  Called by the whole workgroup;
+// returns the count, with every emit's stores done before it returns.
+template <typename Load, typename Pick, typename Emit>
+__device__ int wg_compact(int n, PrepShared& sh, Load load, Pick pick, Emit emit) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int total = 0;
   for (int r0 = 0; r0 < n; r0 += kCompactPer * kPrepThreads) {
     const int i0 = r0 + kCompactPer * tid;
+    decltype(load(0)) v[kCompactPer];
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k)
+      if (i0 + k < n) v[k] = load(i0 + k);
     int pay[kCompactPer], cnt = 0;
 #pragma unroll
     for (int k = 0; k < kCompactPer; ++k) {
-      pay[k] = i0 + k < n ? pick(i0 + k) : -1;
+      pay[k] = i0 + k < n ? pick(i0 + k, v[k]) : -1;
       cnt += pay[k] >= 0;
     }
     const int incl = wave_incl_scan(cnt);
@@ -221,30 +229,91 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
   int32_t* claim_tag = s.tags + kTagClaim * s.NB;
   int32_t* dedupe_tag = s.tags + kTagCloseDedupe * s.NB;
   int32_t* tmp = s.close_list;             // deduplicated claims (scratch until the close phase)
-  int32_t* late = s.close_list + s.cap;    // closing claims past the transient scratch
+  int32_t* late = s.tags + kLateList * s.NB;  // closing claims past the transient scratch (deduplicated: <= NB)
   int32_t* heirs = s.claim_list + s.cap;   // claims staged as heirs, in order
   const int top0 = s.counters[kFreeTop];
 
-  // liveness of persistent slots; close marks
+  int32_t* ccand = s.close_list + s.cap;   // offset-127 blocks, compacted in place into the close list's heirs half
+
+  // liveness of persistent slots (the round's loads in flight together)
   for (int i = tid; i < (s.S_p + 31) / 32; i += kPrepThreads) sh.live[i] = 0;
   __syncthreads();
-  for (int i = tid; i < n_live; i += kPrepThreads) {
-    const int b = live[i];
-    const int w = b >= 0 && b < s.NB ? s.wslot[b] : -1;
-    if (w >= 0 && w < s.S_p) atomicOr(&sh.live[w >> 5], 1u << (w & 31));
+  for (int r0 = 0; r0 < n_live; r0 += kCompactPer * kPrepThreads) {
+    int bl[kCompactPer], w[kCompactPer];
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k) {
+      const int i = r0 + k * kPrepThreads + tid;
+      bl[k] = i < n_live ? live[i] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k) w[k] = bl[k] >= 0 && bl[k] < s.NB ? s.wslot[bl[k]] : -1;
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k)
+      if (w[k] >= 0 && w[k] < s.S_p) atomicOr(&sh.live[w[k] >> 5], 1u << (w[k] & 31));
   }
-  for (int i = tid; i < n_tok; i += kPrepThreads) {
-    const int b = slot_block(s, slots[i], 127);
-    if (b >= 0) close_tag[b] = step;
+
+  // One pass over the slot mapping, no atomics: close marks (offset 127),
+  // and two lists compacted together in input order -- the block of every
+  // offset-0 token into tmp, of every offset-127 token into ccand.  Counts
+  // are packed in one scan (each below 2^16: kScanPer * kPrepThreads
+  // items per round); the next round's slots load while a round is scanned
+  // (the round's barriers wait for LDS only).
+  int n_raw0 = 0, n_raw1 = 0;
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    int64_t nv[kScanPer];
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) nv[k] = kScanPer * tid + k < n_tok ? slots[kScanPer * tid + k] : -1;
+    for (int r0 = 0; r0 < n_tok; r0 += kScanPer * kPrepThreads) {
+      int b0[kScanPer], b1[kScanPer], c = 0;
+#pragma unroll
+      for (int k = 0; k < kScanPer; ++k) {
+        b0[k] = slot_block(s, nv[k], 0);
+        b1[k] = slot_block(s, nv[k], 127);
+        c += (b0[k] >= 0) + ((b1[k] >= 0) << 16);
+      }
+      const int i1 = r0 + kScanPer * (kPrepThreads + tid);
+#pragma unroll
+      for (int k = 0; k < kScanPer; ++k) nv[k] = i1 + k < n_tok ? slots[i1 + k] : -1;
+      const int incl = wave_incl_scan(c);
+      if (lane == 63) sh.wcnt[wave] = incl;
+      lds_barrier();
+      int before = 0, all = 0;
+#pragma unroll
+      for (int q = 0; q < kPrepWaves; ++q) {
+        const int x = sh.wcnt[q];
+        before += q < wave ? x : 0;
+        all += x;
+      }
+      lds_barrier();  // wcnt is rewritten by the next round
+      const int ex = before + incl - c;
+      int r0c = n_raw0 + (ex & 0xFFFF), r1c = n_raw1 + (ex >> 16);
+#pragma unroll
+      for (int k = 0; k < kScanPer; ++k) {
+        if (b0[k] >= 0) tmp[r0c++] = b0[k];
+        if (b1[k] >= 0) {
+          ccand[r1c++] = b1[k];
+          close_tag[b1[k]] = step;
+        }
+      }
+      n_raw0 += all & 0xFFFF;
+      n_raw1 += all >> 16;
+    }
   }
-  __syncthreads();
+  __syncthreads();  // the lists and close marks are visible to the next phases
+
+  // claims: one per block, the first offset-0 token to stamp claim_tag
+  // (compacted in place: a round's items are loaded before any is written)
+  const int n_cand = wg_compact(
+      n_raw0, sh, [&](int i) { return tmp[i]; },
+      [&](int, int b) { return atomicExch(&claim_tag[b], step) != step ? b : -1; },
+      [&](int, int r, int b) { tmp[r] = b; });
 
   // GC: transient slots end with their step; persistent slots of blocks not
   // live go back on the free stack (pushed in block order)
   const int freed = wg_compact(
-      s.NB, sh,
-      [&](int b) {
-        const int w = s.wslot[b];
+      s.NB, sh, [&](int b) { return s.wslot[b]; },
+      [&](int b, int w) {
         if (w >= s.S_p) s.wslot[b] = -1;
         if (w < 0 || w >= s.S_p || ((sh.live[w >> 5] >> (w & 31)) & 1u)) return -1;
         s.wslot[b] = -1;
@@ -253,19 +322,10 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
       [&](int, int r, int w) { s.free_stack[top0 + r] = w; });
   const int top = top0 + freed;
 
-  // claims (offset 0), one per block
-  const int n_cand = wg_compact(
-      n_tok, sh,
-      [&](int i) {
-        const int b = slot_block(s, slots[i], 0);
-        return b >= 0 && atomicExch(&claim_tag[b], step) != step ? b : -1;
-      },
-      [&](int, int r, int b) { tmp[r] = b; });
   // blocks that open and close within the step: transient scratch in order
   const int n_close_claims = wg_compact(
-      n_cand, sh,
-      [&](int i) {
-        const int b = tmp[i];
+      n_cand, sh, [&](int i) { return tmp[i]; },
+      [&](int, int b) {
         return s.wslot[b] < 0 && close_tag[b] == step ? b : -1;
       },
       [&](int, int r, int b) {
@@ -278,9 +338,8 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
   // blocks that stay open: the free stack from its top, then heirs in scratch
   int errors = 0;
   const int n_open_claims = wg_compact(
-      n_cand, sh,
-      [&](int i) {
-        const int b = tmp[i];
+      n_cand, sh, [&](int i) { return tmp[i]; },
+      [&](int, int b) {
         return s.wslot[b] < 0 && close_tag[b] != step ? b : -1;
       },
       [&](int, int r, int b) {
@@ -301,24 +360,24 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
   }
   errors += max(n_late - max(top - n_open_claims, 0), 0);
   __syncthreads();
+
   const int n_claims = wg_compact(
-      n_cand, sh, [&](int i) { return s.wslot[tmp[i]] >= 0 ? tmp[i] : -1; },
+      n_cand, sh, [&](int i) { return tmp[i]; }, [&](int, int b) { return s.wslot[b] >= 0 ? b : -1; },
       [&](int, int r, int b) { s.claim_list[r] = b; });
 
-  // closes (offset 127), one per block holding staging; persistent donors
-  // hand their slot to the heirs in order
+  // closes (offset 127), one per block holding staging (the first token to
+  // stamp dedupe_tag); persistent donors hand their slot to the heirs in
+  // order.  The candidates lie in the heirs half of the close list and are
+  // compacted in place (rank <= index, a round's items loaded first).
   const int n_closes = wg_compact(
-      n_tok, sh,
-      [&](int i) {
-        const int b = slot_block(s, slots[i], 127);
-        return b >= 0 && atomicExch(&dedupe_tag[b], step) != step && s.wslot[b] >= 0 ? b : -1;
-      },
+      n_raw1, sh, [&](int c) { return ccand[c]; },
+      [&](int, int b) { return atomicExch(&dedupe_tag[b], step) != step && s.wslot[b] >= 0 ? b : -1; },
       [&](int, int r, int b) {
         s.close_list[r] = b;
         s.close_list[s.cap + r] = -1;
       });
   const int n_donors = wg_compact(
-      n_closes, sh, [&](int c) { return s.wslot[s.close_list[c]] < s.S_p ? c : -1; },
+      n_closes, sh, [&](int c) { return s.close_list[c]; }, [&](int c, int b) { return s.wslot[b] < s.S_p ? c : -1; },
       [&](int, int d, int c) {
         if (d < n_heirs) s.close_list[s.cap + c] = heirs[d];
       });
@@ -326,14 +385,34 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
 
   // claimed blocks' records -> their staging, raw; freed overflow slots; page fill reset
   const int per = s.L * 2 * s.H;
-  for (int x = tid; x < n_claims * per; x += kPrepThreads) {
-    const int b = s.claim_list[x / per];
-    const int r = x % per, layer = r / (2 * s.H), kvh = r % (2 * s.H);
-    const int64_t idx = ((int64_t)layer * s.NB + b) * 2 * s.H + kvh;
-    ovf_free(s, s.rec_addr[idx]);
-    s.rec_addr[idx] = reinterpret_cast<int64_t>(staging_addr(s, s.wslot[b], layer, kvh));
-    s.rec_len[idx] = kRawVarLen;
-    if (kvh == 0) s.fill[(int64_t)layer * s.NB + b] = 0;
+  const int64_t n_ent = (int64_t)n_claims * per;
+  for (int64_t x0 = 0; x0 < n_ent; x0 += kCompactPer * kPrepThreads) {
+    // each level's loads for the round's entries in flight together
+    int b[kCompactPer], w[kCompactPer];
+    int64_t old[kCompactPer];
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k) {
+      const int64_t x = x0 + k * kPrepThreads + tid;
+      b[k] = x < n_ent ? s.claim_list[x / per] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k) {
+      const int64_t x = x0 + k * kPrepThreads + tid;
+      const int r = (int)(x % per), layer = r / (2 * s.H), kvh = r % (2 * s.H);
+      w[k] = b[k] >= 0 ? s.wslot[b[k]] : -1;
+      old[k] = b[k] >= 0 ? s.rec_addr[((int64_t)layer * s.NB + b[k]) * 2 * s.H + kvh] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kCompactPer; ++k) {
+      if (b[k] < 0) continue;
+      const int64_t x = x0 + k * kPrepThreads + tid;
+      const int r = (int)(x % per), layer = r / (2 * s.H), kvh = r % (2 * s.H);
+      const int64_t idx = ((int64_t)layer * s.NB + b[k]) * 2 * s.H + kvh;
+      ovf_free(s, old[k]);
+      s.rec_addr[idx] = reinterpret_cast<int64_t>(staging_addr(s, w[k], layer, kvh));
+      s.rec_len[idx] = kRawVarLen;
+      if (kvh == 0) s.fill[(int64_t)layer * s.NB + b[k]] = 0;
+    }
   }
   if (tid == 0) {
     const int popped = min(top, n_open_claims + n_late);
@@ -925,9 +1004,9 @@ __global__ void __launch_bounds__(kPrepThreads) commit_kernel(Store s) {
   const int n = s.counters[kCloses];
   const int top = s.counters[kFreeTop];
   const int pushed = wg_compact(
-      n, sh,
-      [&](int c) {
-        const int b = s.close_list[c], heir = s.close_list[s.cap + c];
+      n, sh, [&](int c) { return make_int2(s.close_list[c], s.close_list[s.cap + c]); },
+      [&](int, int2 e) {
+        const int b = e.x, heir = e.y;
         const int w = s.wslot[b];
         s.wslot[b] = -1;
         if (heir >= 0) s.wslot[heir] = w;
