@@ -329,7 +329,8 @@ def encode_bench(torch, args, ordered: bool = False) -> dict:
     eff = (records - int(c[5])) * 32768
     log(f"encode{' (ordered)' if ordered else ''}: {records} records in {ms * 1e3:.0f} us -> {eff / ms / 1e6:.0f} GB/s effective, "
         f"fallbacks {int(c[6])} (spills {int(c[8])}), overflow-full drops {int(c[5])}")
-    return dict(ms=ms, records=records, eff_bytes=eff, read_write_bytes=eff + written, fallbacks=int(c[6]),
+    # HBM traffic: every record is read (the dropped ones too), plus what was written
+    return dict(ms=ms, records=records, eff_bytes=eff, read_write_bytes=records * 32768 + written, fallbacks=int(c[6]),
                 spills=int(c[8]), err_overflow=int(c[5]))
 
 
