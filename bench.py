@@ -211,6 +211,114 @@ def paged_bench(torch, args) -> dict:
     return dict(step_ms=step_ms, bytes=nbytes, valid=valid, splits=splits, max_err=err.max().item())
 
 
+def _timed(torch, args, step) -> float:
+    """ms per call of ``step``, enqueued behind a spinning kernel (GPU time)."""
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream()
+    ms = []
+    for _ in range(2):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(args.steps * 40_000))  # host enqueues while the GPU spins
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1) / args.steps)
+    return ms[-1]
+
+
+def config2_bench(torch, args) -> dict:
+    """BASELINE config 2, MHA mixed-length decode: B16 x H32 x G1, context
+    lengths U[129, 4096] from the seed, 5% outlier channels.  A serving
+    store's state after the prompts: every full block encoded, each partial
+    tail left raw in staging (its open block).  The compressed kernel and the
+    plain BF16 paged kernel run the same step over the same KV, both checked
+    against fp32.  Effective bytes = the K and V the step attends over
+    (2 x sum(len) x H x 128 x 2 B)."""
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+    from fragpack_amd.ops.paged_attn import paged_decode_attention, paged_splits, paged_workspace
+
+    B, H, G = 16, 32, 1
+    rng = np.random.default_rng(args.seed + 2)
+    lens = rng.integers(129, 4097, B).astype(np.int64)
+    pages = -(-lens // T)
+    nb, n_tok, maxp = int(pages.sum()), int(lens.sum()), int(pages.max())
+    scales = channel_scales(rng, H, 0.05)
+    tables = calibrated_tables(rng, H, scales)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+    perm = rng.permutation(nb).astype(np.int64)
+    bt_np = np.zeros((B, maxp), np.int32)
+    slots = []
+    o = 0
+    for b in range(B):
+        blk = perm[o : o + pages[b]]
+        o += pages[b]
+        bt_np[b, : pages[b]] = blk
+        t = np.arange(lens[b])
+        slots.append(blk[t // T] * T + t % T)
+    slots_t = torch.from_numpy(np.concatenate(slots)).to(dev)
+    kv = gen_kv(torch, gen, n_tok, H, torch.from_numpy(scales).float().to(dev))
+    arena = torch.empty((nb, page_bytes(H)), dtype=torch.uint8, device=dev)
+    store = HbmKvStore([arena], H, device_tables(tables, dev), max_tokens=n_tok, staging_slots=B,
+                       overflow_records=8192)
+    store.prepare(slots_t, n_tok, np.zeros(0, np.int32))
+    store.write(0, kv[0], kv[1], slots_t)
+    store.encode(0, int((lens // T).sum()))
+    store.commit()
+    stats = store.stats()
+    # the same KV in a plain paged BF16 cache
+    paged = torch.zeros((2, nb * T, H, D), dtype=torch.bfloat16, device=dev)
+    paged[:, slots_t] = kv
+    del kv
+    bt = torch.from_numpy(bt_np).to(dev)
+    lens_t = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    q = torch.randn((B, H * G, D), generator=gen, device=dev).to(torch.bfloat16)
+    scale = D ** -0.5
+    ref = reference_decode(torch, q, paged, bt.cpu(), lens, H, G, scale)
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    units = decode_units(B, H, sms)
+    o_e, m_e, p_e = workspace_elems(H, units)
+    ws = (torch.empty(o_e, device=dev), torch.empty(m_e, device=dev), torch.empty(p_e, dtype=torch.int32, device=dev))
+    tabs = RecordTables(*store.layer_tables(0))
+    out_c = torch.full_like(q, float("nan"))
+    splits = paged_splits(B, H, int(lens.max()))
+    pws = paged_workspace(B, H, splits, dev)
+    out_p = torch.full_like(q, float("nan"))
+    comp = lambda: decode_attention(q, tabs, bt, lens_t, scale, units, out_c, ws, True)  # noqa: E731
+    plain = lambda: paged_decode_attention(q, paged[0].view(nb, T, H, D), paged[1].view(nb, T, H, D), bt,  # noqa: E731
+                                           lens_t, int(lens.max()), scale, out_p, pws, splits)
+    comp()
+    plain()
+    torch.cuda.synchronize()
+    res = {}
+    for name, out in (("compressed", out_c), ("bf16_paged", out_p)):
+        err = (out.float() - ref).abs()
+        res[name] = {"valid": bool(torch.isfinite(out.float()).all() and (err <= 2e-2 + 1e-2 * ref.abs()).all()),
+                     "max_err": round(err.max().item(), 5)}
+    eff = 2 * n_tok * H * D * 2
+    for name, fn in (("compressed", comp), ("bf16_paged", plain)):
+        ms = _timed(torch, args, fn)
+        res[name].update(us_per_step=round(ms * 1e3, 2), effective_GBps=round(eff / ms / 1e6, 1))
+    rl = store.rec_len[0].cpu().numpy()[perm]
+    coded = int((rl <= 2048).sum())
+    res.update(workload="config 2: MHA decode, B16 x H32 x G1, ragged U[129, 4096], 5% outlier channels",
+               lens_sum=n_tok, blocks=nb, coded_records=coded, records=int(rl.size),
+               encoded=stats.encoded, fallbacks=stats.fallbacks,
+               compressed_step_speedup=round(res["bf16_paged"]["us_per_step"] / res["compressed"]["us_per_step"], 3))
+    log(f"config 2 B16 H32 G1 ragged: compressed {res['compressed']['us_per_step']} us/step "
+        f"({res['compressed']['effective_GBps']} GB/s effective), BF16 paged {res['bf16_paged']['us_per_step']} us/step, "
+        f"{coded}/{rl.size} records coded, valid {res['compressed']['valid']}/{res['bf16_paged']['valid']}")
+    del paged, store, arena
+    torch.cuda.empty_cache()
+    return res
+
+
 def prefill_bench(torch, args) -> dict:
     """Causal prefill over config 4's prompts: ``--prefill-seqs`` x
     ``--prefill-len`` tokens, 32 query heads over 8 KV heads (GQA 4), on a
@@ -603,6 +711,7 @@ def main() -> None:
     ap.add_argument("--no-layer-step", action="store_true",
                     help="skip the per-layer serving step legs (write, attention, encode)")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the plain read / copy / fill rate legs")
+    ap.add_argument("--no-config2", action="store_true", help="skip the config-2 (MHA, ragged) decode leg")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the batch-64 context sweep (8K and 16K, both arms) beside config 4's 32K")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -660,6 +769,12 @@ def main() -> None:
                 large_raw.pop(k)
             torch.cuda.empty_cache()
             large_paged = paged_bench(torch, largs)
+    config2 = None
+    if not args.no_config2:
+        torch.cuda.empty_cache()
+        c2args = argparse.Namespace(**vars(args))
+        c2args.steps, c2args.warmup = 50, 5
+        config2 = config2_bench(torch, c2args)
     layer_steps = []
     if not args.no_layer_step:
         # one layer of a serving decode step: config 1's shape and config 4's
@@ -773,6 +888,8 @@ def main() -> None:
                 "hbm_GBps": round(large_raw["algo_bytes"] / (large_raw["kern_ms"] / 1e3) / 1e9, 1)}
     if sweep:
         line["context_sweep"] = sweep
+    if config2 is not None:
+        line["config2"] = config2
     if layer_steps:
         line["layer_step"] = layer_steps
     if enc is not None:
