@@ -48,6 +48,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;     // wavefronts per workgroup = slabs per record
+constexpr int kBtLds = 1024;  // block-table entries a planning launch may hold in LDS
 constexpr int kAttnPerCu = 3;  // resident workgroups per CU (kWaves = SIMDs per CU; VGPR budget 512 / 3)
 constexpr float kLazyMax = 8.f;    // log2 headroom of the speculative softmax reference
 constexpr int kTileRow = 4 * 4 * 16 + 16;   // one head's row of a fragment tile, padded by a chunk
@@ -73,6 +74,7 @@ struct AttnParams {
   int ud_off;  // int32 offset of the unit descriptors in plan
   int slots;   // resident workgroups of this kernel on the device
   int inline_plan;  // 1: every workgroup plans for itself (batch <= 64)
+  int bt_lds;       // inline plan and the whole block table (batch x bt_stride <= kBtLds) read into LDS
   float scale_log2;
   // Optional append of each sequence's new token (decode rows: position
   // seq_len - 1) into its open block's raw record before attention reads it;
@@ -595,7 +597,15 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
   // the work plan: planned here (inline) or read from the plan workspace
   InlinePlan ip{0, 0, 0, 0, 1, 0};
+  // Planning launches with a small block table read all of it into LDS
+  // beside the plan's sequence lengths, so a unit's page ids need no
+  // global round trip after the plan is known.
+  __shared__ int bt_s[kInlinePlan ? kBtLds : 1];
+  const bool bt_lds = kInlinePlan && p.bt_lds;
+  if (bt_lds)
+    for (int i = threadIdx.x; i < p.batch * (int)p.bt_stride; i += 64 * kWaves) bt_s[i] = p.block_table[i];
   if constexpr (kInlinePlan) ip = inline_plan(p, lane);
+  if (bt_lds) __syncthreads();
   const int used = kInlinePlan ? ip.used : uniform(p.plan[1]);  // units in use
   const int ppc = ip.ppc;
   if constexpr (kInlinePlan) {
@@ -641,7 +651,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       seq = uniform(sh.plan[w][2][b]);
       p0 = (unit - first) * ppc;
       npages = min(uniform(sh.plan[w][3][b]), p0 + ppc) - p0;
-      blk0 = uniform(p.block_table[(int64_t)b * p.bt_stride + p0]);
+      const int bt0 = b * (int)p.bt_stride + p0;  // (bt_lds: < batch x bt_stride <= kBtLds)
+      blk0 = uniform(bt_lds ? bt_s[bt0] : p.block_table[(int64_t)b * p.bt_stride + p0]);
       if (h == 0 && threadIdx.x == 0) {
         // this unit's plan entries for later calls
         int32_t* plan = p.plan;
@@ -649,7 +660,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         plan[3 + 2 * unit] = p0;
         int4* ud = reinterpret_cast<int4*>(plan + p.ud_off + 8 * unit);
         ud[0] = make_int4(b, p0, npages, seq);
-        ud[1] = make_int4(first, chunks, blk0, npages > 1 ? p.block_table[(int64_t)b * p.bt_stride + p0 + 1] : 0);
+        ud[1] = make_int4(first, chunks, blk0,
+                          npages > 1 ? (bt_lds ? bt_s[bt0 + 1] : p.block_table[(int64_t)b * p.bt_stride + p0 + 1]) : 0);
       }
     } else {
       // unit descriptor: b, first page, pages, context, first unit of b,
@@ -681,7 +693,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // block ids of the unit's first 64 pages (one per lane), in the same hop
     // as page 0's record tables, which come straight from the descriptor's
     // block id
-    const int blk = load_block(bt, 0, npages, lane);
+    const int blk = bt_lds && kInlinePlan ? (lane < npages ? bt_s[(b * (int)p.bt_stride + p0 + lane) % kBtLds] : -1)
+                                          : load_block(bt, 0, npages, lane);
     RecRef kr, vr;
     {
       const int64_t kidx = ((int64_t)blk0 * 2) * p.kvh + h;
@@ -957,9 +970,11 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   const int slots = decode_slots();
   FP_CHECK(slots > 0, "cannot query the device's compute-unit count");
   p.slots = slots;
-  // replan 2: plan inside the attention kernel (batch <= 64; the merge
+  // replan 2 / 3: plan inside the attention kernel (batch <= 64; the merge
   // counters must be as a previous completed call left them, i.e. zero)
-  p.inline_plan = replan == 2 && batch <= 64;
+  FP_CHECK(replan >= 0 && replan <= 3, "replan must be 0, 1, 2 or 3");
+  p.inline_plan = (replan == 2 || replan == 3) && batch <= 64;
+  p.bt_lds = replan == 3 && p.inline_plan && batch * bt_stride <= kBtLds;
   if (replan && !p.inline_plan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
                        plan_elems, (int)batch, (int)units, (int)kv_heads, slots);

@@ -173,6 +173,11 @@ class Extension:
         mode = 0
         if replan:
             mode = 2 if getattr(plan, "_fp_counters_zeroed", False) else 1
+            # 3: the kernel may read the whole (small) block table -- only if
+            # its storage holds B rows of stride entries from the view's start
+            if mode == 2 and B * bst[0] <= 1024 and \
+                    block_table.untyped_storage().nbytes() >= (block_table.storage_offset() + B * bst[0]) * 4:
+                mode = 3
         args = (
             _dev(q, "q"), qst[0], B, kvh, group, _dev(rec_addr, "rec_addr"), _dev(rec_len, "rec_len"),
             _dev(plut, "plut"), _dev(slut, "slut"), _dev(block_table, "block_table"), bst[0],

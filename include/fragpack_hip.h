@@ -71,7 +71,10 @@ int fp_abi_version(void);
  *   replan      0: reuse the plan in the workspace; 1: plan with a planner
  *               launch (also zeroes the merge counters); 2: plan inside the
  *               attention kernel when batch <= 64 (else as 1) -- the merge
- *               counters must be zero, as any completed call leaves them
+ *               counters must be zero, as any completed call leaves them;
+ *               3: as 2, and block_table holds batch * bt_stride readable
+ *               entries (the kernel may read all of them when there are at
+ *               most 1024)
  */
 int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
                     const int64_t* rec_addr, const int32_t* rec_len, const uint32_t* plut,

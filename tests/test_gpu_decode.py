@@ -118,3 +118,41 @@ def test_graph_replay_changed_lengths():
         case.lens = lt
         _check(out.float().cpu().numpy(), kvgen.reference_attention(case), lt)
     del arena
+
+
+def test_planning_launch_block_table_forms():
+    """Planning inside the kernel with the block table read whole into LDS
+    (a small table whose storage covers batch x stride entries) and read
+    from global memory (a column view at a storage offset; a table past
+    1024 entries) give bit-identical outputs, equal to fp32."""
+    import torch
+
+    from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
+
+    lens = [300, 2000, 1, 513, 0, 129]
+    case = kvgen.decode_case(seed=41, batch=len(lens), heads=2, group=8, lens=lens)
+    q, rec_addr, rec_len, plut, slut, bt, lens_t, arena = kvgen.upload(case)
+    B, width = bt.shape
+    units = decode_units(B, 2, torch.cuda.get_device_properties(q.device).multi_processor_count)
+    tabs = RecordTables(rec_addr, rec_len, plut, slut)
+    view_parent = torch.zeros((B, width + 5), dtype=torch.int32, device=q.device)
+    view_parent[:, 3 : 3 + width] = bt
+    wide = torch.zeros((B, 1100 // B + width), dtype=torch.int32, device=q.device)
+    wide[:, :width] = bt
+    outs = []
+    for name, table in (("whole table in LDS", bt.contiguous()), ("offset view", view_parent[:, 3 : 3 + width]),
+                        ("wide table", wide)):
+        print("block table form:", name, flush=True)
+        opart, ml, plan = workspace_elems(2, units)
+        ws = (torch.empty(opart, device=q.device), torch.empty(ml, device=q.device),
+              torch.empty(plan, dtype=torch.int32, device=q.device))
+        out = torch.full_like(q, float("nan"))
+        for _ in range(3):  # the first call launches the planner; later ones plan in the kernel
+            decode_attention(q, tabs, table, lens_t, case.scale, units, out, ws, True)
+        torch.cuda.synchronize()
+        outs.append(out.clone())
+    ref = kvgen.reference_attention(case)
+    for out in outs:
+        _check(out.float().cpu().numpy(), ref, lens)
+        assert torch.equal(out.view(torch.int16), outs[0].view(torch.int16))
+    del arena
