@@ -424,7 +424,6 @@ struct AttnShared {
   uint8_t pt[kTileBytes];      // P tile
   uint8_t qt[kTileBytes];      // Q tile, even-odd slot order
   float red[kWaves][8];        // per-wave page max / final l per head
-  int plan[kWaves][4][64];     // inline plan per wave: first unit, chunks, context, pages by sequence
   int last;
 };
 
@@ -601,6 +600,9 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // beside the plan's sequence lengths, so a unit's page ids need no
   // global round trip after the plan is known.
   __shared__ int bt_s[kInlinePlan ? kBtLds : 1];
+  // the inline plan per wave: first unit, chunks, context, pages by sequence
+  __shared__ int plan_s[kInlinePlan ? kWaves : 1][4][64];
+  int(&wplan)[4][64] = plan_s[kInlinePlan ? w : 0];  // this wave's rows
   const bool bt_lds = kInlinePlan && p.bt_lds;
   if (bt_lds)
     for (int i = threadIdx.x; i < p.batch * (int)p.bt_stride; i += 64 * kWaves) bt_s[i] = p.block_table[i];
@@ -611,10 +613,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   if constexpr (kInlinePlan) {
     // the per-sequence plan goes to this wave's LDS rows (read back by
     // sequence), so its four registers are free during the page loop
-    sh.plan[w][0][lane] = ip.first;
-    sh.plan[w][1][lane] = ip.cnt;
-    sh.plan[w][2][lane] = ip.len;
-    sh.plan[w][3][lane] = ip.n;
+    wplan[0][lane] = ip.first;
+    wplan[1][lane] = ip.cnt;
+    wplan[2][lane] = ip.len;
+    wplan[3][lane] = ip.n;
     // lanes read each other's rows below: order the stores before those
     // reads for the compiler too (the wave's LDS accesses are in order)
     wave_lds_sync();
@@ -644,13 +646,13 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     int b, p0, npages, seq, first, chunks, blk0;
     if constexpr (kInlinePlan) {
       // the last live sequence whose first unit is <= unit owns it
-      const uint64_t own = __ballot(lane < p.batch && sh.plan[w][1][lane] > 0 && sh.plan[w][0][lane] <= unit);
+      const uint64_t own = __ballot(lane < p.batch && wplan[1][lane] > 0 && wplan[0][lane] <= unit);
       b = 63 - __builtin_clzll(own);
-      first = uniform(sh.plan[w][0][b]);
-      chunks = uniform(sh.plan[w][1][b]);
-      seq = uniform(sh.plan[w][2][b]);
+      first = uniform(wplan[0][b]);
+      chunks = uniform(wplan[1][b]);
+      seq = uniform(wplan[2][b]);
       p0 = (unit - first) * ppc;
-      npages = min(uniform(sh.plan[w][3][b]), p0 + ppc) - p0;
+      npages = min(uniform(wplan[3][b]), p0 + ppc) - p0;
       const int bt0 = b * (int)p.bt_stride + p0;  // (bt_lds: < batch x bt_stride <= kBtLds)
       blk0 = uniform(bt_lds ? bt_s[bt0] : p.block_table[(int64_t)b * p.bt_stride + p0]);
       if (h == 0 && threadIdx.x == 0) {
@@ -896,7 +898,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
     for (int b = w; b < p.batch; b += kWaves) {
-      const int cnt = kInlinePlan ? sh.plan[w][1][b] : p.plan[3 + 2 * p.units + 2 * b];
+      const int cnt = kInlinePlan ? wplan[1][b] : p.plan[3 + 2 * p.units + 2 * b];
       if (cnt != 0) continue;
       uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)h * p.group * kDim);
       for (int x = lane; x < p.group * kDim / 2; x += 64) orow[x] = 0u;
