@@ -452,3 +452,72 @@ def test_blob_import_rejects_bad_blobs_untouched():
     assert _import(dst, blobs, [0], [10]) == [4]
     assert _overflow_in_use(dst) == 1
     assert torch.equal(dst.store.rec_addr[0, 10], before[0][0, 10])
+
+
+def test_fused_write_encode_degenerate_steps():
+    """write_encode with nothing to close (the write alone), with no tokens
+    (the encode alone) and with padding slots (-1) leaves the same records
+    and counters as the separate calls on a twin store."""
+    import torch
+
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+
+    H, NB = 2, 6
+    rng = np.random.default_rng(77)
+    dump = kvgen.bf16_bits(rng.standard_normal((4, 1, 2, T, H, D)) * 0.5)
+    from fragpack_amd.compression.attn_tables import calibrate
+
+    tables = device_tables(calibrate(dump), torch.device("cuda"))
+
+    def twin():
+        arena = torch.zeros((NB, page_bytes(H)), dtype=torch.uint8, device="cuda")
+        return HbmKvStore([arena], H, tables, max_tokens=512, staging_slots=2, overflow_records=8), arena
+
+    (a, arena_a), (b, arena_b) = twin(), twin()
+    kv = torch.from_numpy(kvgen.bf16_bits(rng.standard_normal((2, 3 * T, H, D)) * 0.5).view(np.int16)).cuda()
+    kv = kv.view(torch.bfloat16)
+    # step 1: block 0 rows 0..99 and block 1 rows 0..4 (nothing closes), with padding
+    slots = torch.tensor([-1] + list(range(100)) + [128 + r for r in range(5)] + [-1], dtype=torch.int64,
+                         device="cuda")
+    k, v = kv[0, : slots.numel()], kv[1, : slots.numel()]
+    for st in (a, b):
+        st.prepare(slots, slots.numel(), np.zeros(0, np.int32))
+    a.write(0, k, v, slots)
+    a.encode(0, 0)
+    b.write_encode(0, k, v, slots, 0)
+    for st in (a, b):
+        st.commit()
+    # step 2: block 0 rows 100..127 close it; block 1 row 5 stays open
+    slots2 = torch.tensor(list(range(100, 128)) + [133, -1], dtype=torch.int64, device="cuda")
+    k2, v2 = kv[0, 200 : 200 + slots2.numel()], kv[1, 200 : 200 + slots2.numel()]
+    live = np.array([0, 1], np.int32)
+    for st in (a, b):
+        st.prepare(slots2, slots2.numel(), live)
+    a.write(0, k2, v2, slots2)
+    a.encode(0, 2)
+    b.write_encode(0, k2, v2, slots2, 2)
+    # step 3: no tokens; the fused call only encodes (nothing is left to close)
+    for st in (a, b):
+        st.commit()
+        st.prepare(torch.empty(0, dtype=torch.int64, device="cuda"), 0, np.array([1], np.int32))
+    a.encode(0, 1)
+    b.write_encode(0, kv[0, :0], kv[1, :0], torch.empty(0, dtype=torch.int64, device="cuda"), 1)
+    for st in (a, b):
+        st.commit()
+    torch.cuda.synchronize()
+    assert a.stats() == b.stats() and a.stats().encoded == 2 * H
+    ids = torch.arange(2, dtype=torch.int32, device="cuda")
+    got = []
+    for st in (a, b):
+        wk = torch.empty((2, T, H, D), dtype=torch.bfloat16, device="cuda")
+        wv = torch.empty_like(wk)
+        st.gather(0, ids, wk, wv)
+        got.append((wk.view(torch.int16).clone(), wv.view(torch.int16).clone()))
+    want_k = torch.cat((kv[0, 1:101], kv[0, 200:228]))  # block 0: step 1 rows 0..99, step 2 rows 100..127
+    assert torch.equal(got[1][0][0], want_k.view(torch.int16))
+    assert torch.equal(got[0][0][:, :6], got[1][0][:, :6]) and torch.equal(got[0][1][:, :6], got[1][1][:, :6])
+    assert torch.equal(got[0][0][0], got[1][0][0]) and torch.equal(got[0][1][0], got[1][1][0])
+    # block 1: rows 0..4 from step 1, row 5 from step 2
+    want_k1 = torch.cat((kv[0, 101:106], kv[0, 228:229]))
+    assert torch.equal(got[1][0][1, :6], want_k1.view(torch.int16))
