@@ -228,12 +228,13 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
   int32_t* close_tag = s.tags + kTagClose * s.NB;
   int32_t* claim_tag = s.tags + kTagClaim * s.NB;
   int32_t* dedupe_tag = s.tags + kTagCloseDedupe * s.NB;
-  int32_t* tmp = s.close_list;             // deduplicated claims (scratch until the close phase)
-  int32_t* late = s.tags + kLateList * s.NB;  // closing claims past the transient scratch (deduplicated: <= NB)
-  int32_t* heirs = s.claim_list + s.cap;   // claims staged as heirs, in order
+  // Lists of this step, in space the state already has (every list holds at
+  // most n_tok <= list_cap entries, or at most NB once deduplicated):
+  int32_t* tmp = s.close_list;                // offset-0 blocks, then the deduplicated claims (until the closes)
+  int32_t* ccand = s.close_list + s.cap;      // offset-127 blocks, compacted in place into the closes' heir column
+  int32_t* late = s.tags + kLateList * s.NB;  // closing claims past the transient scratch
+  int32_t* heirs = s.claim_list + s.cap;      // claims staged as heirs, in order
   const int top0 = s.counters[kFreeTop];
-
-  int32_t* ccand = s.close_list + s.cap;   // offset-127 blocks, compacted in place into the close list's heirs half
 
   // liveness of persistent slots (the round's loads in flight together)
   for (int i = tid; i < (s.S_p + 31) / 32; i += kPrepThreads) sh.live[i] = 0;
