@@ -319,6 +319,87 @@ def config2_bench(torch, args) -> dict:
     return res
 
 
+def store_kernels_bench(torch, args) -> dict:
+    """The store's other kernels at config 4's record shape (H8, one layer),
+    each timed on device-resident data against the 8 TB/s HBM roofline:
+    gather (2048 blocks decoded to token-major BF16), block-blob export and
+    import of the same blocks, and the batch codec (8192 records encoded
+    from token-major BF16, then decoded back).  Bytes per launch = what the
+    kernel must read plus what it writes.  Checked: the import's destination
+    gathers back bit-identical to the source, and decode(encode(x)) == x."""
+    from fragpack_amd.compression import attn_page as ap
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops.fragpack_ext import extension
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+
+    H, nb = 8, 2048
+    dev = torch.device("cuda")
+    rng = np.random.default_rng(args.seed + 5)
+    scales = channel_scales(rng, H, 0.02)
+    tables = calibrated_tables(rng, H, scales)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 5)
+    scales_t = torch.from_numpy(scales).float().to(dev)
+    store, arena, _ = build_store(torch, H, nb, tables, gen, scales_t, fill_blocks=64)
+    ids = torch.arange(nb, dtype=torch.int32, device=dev)
+    rl = store.rec_len[0].cpu().numpy()
+    comp = int(np.where(rl > 2048, 32768, DENSE + rl).sum())
+    bf16 = nb * 2 * H * 32768
+    res = {"workload": f"{nb} blocks x {2 * H} records (H8 K/V, one layer), batch codec {nb * 4} records"}
+
+    def record(name, ms, nbytes, **extra):
+        gbps = nbytes / ms / 1e6
+        res[name] = {"us": round(ms * 1e3, 1), "bytes": int(nbytes), "GBps": round(gbps, 1),
+                     "frac_of_8TBps": round(gbps / 8000.0, 4), **extra}
+
+    wk = torch.empty((nb, T, H, D), dtype=torch.bfloat16, device=dev)
+    wv = torch.empty_like(wk)
+    record("gather", _timed(torch, args, lambda: store.gather(0, ids, wk, wv)), comp + bf16)
+    stride = store.blob_stride
+    blobs = torch.empty(nb * stride, dtype=torch.uint8, device=dev)
+    blob_bytes = int(store.export_blocks(ids, blobs, stride).sum().item())
+    record("export", _timed(torch, args, lambda: store.export_blocks(ids, blobs, stride)), comp + blob_bytes)
+    arena2 = torch.empty((nb, page_bytes(H)), dtype=torch.uint8, device=dev)
+    dst = HbmKvStore([arena2], H, device_tables(tables, dev), max_tokens=64 * T, staging_slots=1,
+                     overflow_records=8192)
+    offs = torch.arange(nb, dtype=torch.int64, device=dev) * stride
+    ok = bool((dst.import_blocks(blobs, offs, ids) == 0).all().item())
+    record("import", _timed(torch, args, lambda: dst.import_blocks(blobs, offs, ids)), blob_bytes + comp)
+    wk2, wv2 = torch.empty_like(wk), torch.empty_like(wv)
+    dst.gather(0, ids, wk2, wv2)
+    res["import"]["gather_bitexact"] = ok and torch.equal(wk.view(torch.int16), wk2.view(torch.int16)) and \
+        torch.equal(wv.view(torch.int16), wv2.view(torch.int16))
+    del wk2, wv2, blobs, dst, arena2
+    # batch codec: records (kv, block, head) of fresh KV, token-major [n, 128, 128]
+    blocks = nb // 4
+    kv = gen_kv(torch, gen, blocks * T, H, scales_t).view(2, blocks, T, H, D)
+    raw = kv.permute(0, 1, 3, 2, 4).contiguous().view(-1, T, D)  # [2 * blocks * H, 128 tok, 128 dim]
+    n = raw.size(0)
+    kvf = torch.arange(n, device=dev, dtype=torch.int32) // (blocks * H)
+    tab = (kvf * H + torch.arange(n, device=dev, dtype=torch.int32) % H).to(torch.int32)
+    tabs = tables.reshape(-1, ap.TABLE_ENTRIES)
+    ranks = torch.from_numpy(np.stack([ap.rank_of(t) for t in tabs])).to(dev)
+    plut = torch.from_numpy(np.array([ap.primary_lut(t) for t in tabs], np.uint32).view(np.int32)).to(dev)
+    slut = torch.from_numpy(np.stack([np.frombuffer(ap.secondary_lut(t), np.uint8) for t in tabs])).to(dev)
+    out = torch.empty(n * 32768, dtype=torch.uint8, device=dev)
+    lens = torch.empty(n, dtype=torch.int32, device=dev)
+    ext = extension()
+    enc = lambda: ext.encode_records(raw, kvf, ranks, tab, out, lens)  # noqa: E731
+    enc()
+    torch.cuda.synchronize()
+    written = int(lens.to(torch.int64).sum().item())
+    record("encode_records", _timed(torch, args, enc), n * 32768 + written)
+    addr = out.data_ptr() + 32768 * torch.arange(n, dtype=torch.int64, device=dev)
+    vlen = (lens - DENSE).to(torch.int32)
+    back = torch.empty((n, T, D), dtype=torch.int16, device=dev)
+    dec = lambda: ext.decode_records(addr, vlen, kvf, plut, slut, tab, back)  # noqa: E731
+    record("decode_records", _timed(torch, args, dec), written + n * 32768)
+    res["decode_records"]["round_trip_bitexact"] = bool(torch.equal(back, raw.view(torch.int16)))
+    log("store kernels: " + ", ".join(f"{k} {v['us']} us {v['GBps']} GB/s" for k, v in res.items() if isinstance(v, dict)))
+    del store, arena, wk, wv, kv, raw, out, back
+    torch.cuda.empty_cache()
+    return res
+
+
 def prefill_bench(torch, args) -> dict:
     """Causal prefill over config 4's prompts: ``--prefill-seqs`` x
     ``--prefill-len`` tokens, 32 query heads over 8 KV heads (GQA 4), on a
@@ -712,6 +793,8 @@ def main() -> None:
                     help="skip the per-layer serving step legs (write, attention, encode)")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the plain read / copy / fill rate legs")
     ap.add_argument("--no-config2", action="store_true", help="skip the config-2 (MHA, ragged) decode leg")
+    ap.add_argument("--no-store-kernels", action="store_true",
+                    help="skip the gather / blob export-import / batch codec leg")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the batch-64 context sweep (8K and 16K, both arms) beside config 4's 32K")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -769,6 +852,12 @@ def main() -> None:
                 large_raw.pop(k)
             torch.cuda.empty_cache()
             large_paged = paged_bench(torch, largs)
+    store_kernels = None
+    if not args.no_store_kernels:
+        torch.cuda.empty_cache()
+        skargs = argparse.Namespace(**vars(args))
+        skargs.steps, skargs.warmup = 10, 2
+        store_kernels = store_kernels_bench(torch, skargs)
     config2 = None
     if not args.no_config2:
         torch.cuda.empty_cache()
@@ -890,6 +979,8 @@ def main() -> None:
         line["context_sweep"] = sweep
     if config2 is not None:
         line["config2"] = config2
+    if store_kernels is not None:
+        line["store_kernels"] = store_kernels
     if layer_steps:
         line["layer_step"] = layer_steps
     if enc is not None:
