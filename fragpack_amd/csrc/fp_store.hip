@@ -1116,12 +1116,25 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
                                                                  const uint8_t* rank_of, const int32_t* tab_idx,
                                                                  uint8_t* out, int32_t* lens) {
   __shared__ EncShared sh;
+  // the token-major record, staged with coalesced 16-byte loads; rows padded
+  // by 8 bytes so the column reads of V records spread over the banks
+  constexpr int kRowElems = kDim + 4;
+  __shared__ __align__(16) uint16_t rec[kTokens * kRowElems];
   const int i = blockIdx.x, tid = threadIdx.x;
   const int kv = kvs[i];
   const uint16_t* src = raw + (int64_t)i * kTokens * kDim;
   sh.tb[tid] = table_byte(rank_of[(int64_t)tab_idx[i] * 256 + tid]);
   for (int x = tid; x < kVarCap / 4; x += kThreads) sh.var32[x] = 0;
-  // thread tid's kernel-order words from the token-major record
+#pragma unroll
+  for (int k = 0; k < kTokens * kDim / 8 / kThreads; ++k) {
+    const int e = 8 * (k * kThreads + tid), row = e / kDim, col = e % kDim;  // 16-byte piece
+    const uint4 v = *reinterpret_cast<const uint4*>(src + e);
+    uint2* d = reinterpret_cast<uint2*>(rec + row * kRowElems + col);  // 8-byte aligned (padded rows)
+    d[0] = make_uint2(v.x, v.y);
+    d[1] = make_uint2(v.z, v.w);
+  }
+  __syncthreads();
+  // thread tid's kernel-order words
   const int w = tid >> 5, g = (tid >> 2) & 7, c = tid & 3;
   uint4 wd[8];
 #pragma unroll
@@ -1132,9 +1145,9 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
       const int j = i4 >> 1, f = i4 & 1;
       const int row = 16 * w + 8 * j + g, col = 16 * st + 8 * f + 2 * c;
       if (kv == 0) {
-        d[i4] = *reinterpret_cast<const uint32_t*>(src + row * kDim + col);
+        d[i4] = *reinterpret_cast<const uint32_t*>(rec + row * kRowElems + col);
       } else {
-        d[i4] = (uint32_t)src[col * kDim + row] | ((uint32_t)src[(col + 1) * kDim + row] << 16);
+        d[i4] = (uint32_t)rec[col * kRowElems + row] | ((uint32_t)rec[(col + 1) * kRowElems + row] << 16);
       }
     }
     wd[st] = make_uint4(d[0], d[1], d[2], d[3]);
