@@ -38,6 +38,8 @@ enum : int {
 enum : int { kLateList = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
 
 constexpr int kThreads = 256;
+constexpr int kXcds = 8;    // XCDs of an MI355X (each with its own L2)
+constexpr int kWriteSlabItems = 1 << 14;  // from this many (token, head) items a write takes the slab path
 constexpr int kEncodeWgPerCu = 4;  // resident encode workgroups per CU (LDS: 32 KB stage + 6 KB each)
 
 struct Store {
@@ -432,8 +434,7 @@ __global__ void __launch_bounds__(kPrepThreads) prepare_kernel(Store s, const in
 // (2p, 2p+1) of K (one u32: both scalars are in the same kernel-order word)
 // and of V (two u16: a V pair belongs to two threads) into the raw
 // kernel-order staging record.
-__device__ __forceinline__ void put_k_row(uint8_t* rec, const uint16_t* krow, int off, int p) {
-  const uint32_t val = *reinterpret_cast<const uint32_t*>(krow + 2 * p);
+__device__ __forceinline__ void store_k_pair(uint8_t* rec, uint32_t val, int off, int p) {
   // K: token off = 16 tw + 8 j + g, dim 2p = 16 st + 8 f + 2 c
   const int st = p >> 3, f = (p >> 2) & 1, c = p & 3;
   const int tw = off >> 4, j = (off >> 3) & 1, g = off & 7;
@@ -441,8 +442,7 @@ __device__ __forceinline__ void put_k_row(uint8_t* rec, const uint16_t* krow, in
   *reinterpret_cast<uint32_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f)) = val;
 }
 
-__device__ __forceinline__ void put_v_row(uint8_t* rec, const uint16_t* vrow, int off, int p) {
-  const uint32_t val = *reinterpret_cast<const uint32_t*>(vrow + 2 * p);
+__device__ __forceinline__ void store_v_pair(uint8_t* rec, uint32_t val, int off, int p) {
   // V: token off = 16 st + 8 f + 2 c + e, dim d = 16 tw + 8 j + g
   const int st = off >> 4, f = (off >> 3) & 1, c = (off >> 1) & 3, e = off & 1;
 #pragma unroll
@@ -452,6 +452,14 @@ __device__ __forceinline__ void put_v_row(uint8_t* rec, const uint16_t* vrow, in
     const int t = 32 * tw + 4 * g + c;
     *reinterpret_cast<uint16_t*>(rec + 16 * (256 * st + t) + 2 * (4 * j + 2 * f + e)) = (uint16_t)(val >> (16 * q));
   }
+}
+
+__device__ __forceinline__ void put_k_row(uint8_t* rec, const uint16_t* krow, int off, int p) {
+  store_k_pair(rec, *reinterpret_cast<const uint32_t*>(krow + 2 * p), off, p);
+}
+
+__device__ __forceinline__ void put_v_row(uint8_t* rec, const uint16_t* vrow, int off, int p) {
+  store_v_pair(rec, *reinterpret_cast<const uint32_t*>(vrow + 2 * p), off, p);
 }
 
 // The step's new tokens as the write hands them over (element strides).
@@ -490,8 +498,121 @@ __device__ __forceinline__ void write_item(const Store& s, const StepTokens& tk,
   put_v_row(staging_addr(s, w, layer, s.H + h), tk.v + tok * tk.vs0 + h * tk.vs1, off, p);
 }
 
+// Workgroups are dealt to the 8 XCDs round-robin; the grid is a multiple of
+// 8 and XCD x takes the x-th contiguous eighth of the grid.
+__device__ __forceinline__ int xcd_contiguous_wg() {
+  const int per = (int)gridDim.x / kXcds;
+  return ((int)blockIdx.x % kXcds) * per + (int)blockIdx.x / kXcds;
+}
+
+// One wave per (token, head) item: steps of few tokens.
 __global__ void __launch_bounds__(kThreads) write_kernel(Store s, StepTokens tk, int layer) {
-  write_item(s, tk, layer, blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6), false);
+  write_item(s, tk, layer, xcd_contiguous_wg() * (kThreads / 64) + (threadIdx.x >> 6), false);
+}
+
+// Large steps.  A 16-byte chunk of a kernel-order record holds two K tokens
+// x 4 dims or four V tokens x 2 dims, all of one 16-token slab (token
+// offsets 16 st .. 16 st + 15), so per-token stores are 2- and 4-byte
+// pieces scattered over 8 (K) or 32 (V) lines.  Here each wave owns 16
+// consecutive tokens of the step.  A token whose whole slab the step writes
+// (16 tokens with consecutive slots from an offset that is a multiple of 16)
+// is written by the wave owning the slab's first token: per record, the 16
+// rows are loaded coalesced into LDS and leave as whole 16-byte chunks, 4 KB
+// contiguous (V) or 8 runs of 512 B (K).  Other tokens go through the
+// per-(token, head) path.  Each wave handles one record (kv, head) of its
+// 16 tokens: the 2H waves of a window are neighbours, on one XCD.  The
+// step's K and V rows must be 16-byte aligned.
+constexpr int kSlab = 16;
+constexpr int kSlabRow = 2 * kDim + 16;  // bytes per staged row (padded: 68 dwords)
+
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+  asm volatile("" ::: "memory");
+}
+
+__global__ void __launch_bounds__(kThreads) write_slab_kernel(Store s, StepTokens tk, int layer) {
+  __shared__ __align__(16) uint8_t stage[kThreads / 64][kSlab * kSlabRow];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int job = xcd_contiguous_wg() * (kThreads / 64) + wave;
+  const int rec = job % (2 * s.H);
+  const int t0 = job / (2 * s.H) * kSlab;
+  if (t0 >= tk.n) return;
+  const bool is_v = rec >= s.H;
+  const int h = is_v ? rec - s.H : rec;
+  // slots of tokens t0 - 16 .. t0 + 31 (lanes 0..47); -1 past either end
+  const int ti = t0 - kSlab + lane;
+  const int64_t sl = lane < 3 * kSlab && ti >= 0 && ti < tk.n ? tk.slots[ti] : -1;
+  const int64_t nxt = __shfl_down(sl, 1, 64);
+  const uint64_t run = __ballot(lane < 3 * kSlab - 1 && sl >= 0 && nxt == sl + 1);  // bit i: i -> i+1 consecutive
+  // a token is covered when its slab's first token s0 and the 15 steps after it are consecutive
+  const int r = (int)(sl & (kSlab - 1));
+  const int s0 = lane - r;
+  const bool covered = sl >= 0 && s0 >= 0 && ((run >> s0) & 0x7fffull) == 0x7fffull;
+  const bool mine = lane >= kSlab && lane < 2 * kSlab && ti < tk.n;
+  uint64_t loose = __ballot(mine && sl >= 0 && !covered);
+  const uint64_t start = __ballot(mine && covered && r == 0);
+  uint8_t* lds = stage[wave];
+  const int p = lane;
+  // per-(token, head) path for tokens of partly written slabs
+  while (loose) {
+    const int bit = __builtin_ctzll(loose);
+    loose &= loose - 1;
+    const int64_t tsl = __shfl(sl, bit, 64);
+    const int b = (int)(tsl >> 7), off = (int)(tsl & 127);
+    if (b >= s.NB) continue;
+    const int w = s.wslot[b];
+    if (w < 0) continue;
+    const int tok = t0 - kSlab + bit;
+    if (is_v)
+      put_v_row(staging_addr(s, w, layer, rec), tk.v + tok * tk.vs0 + h * tk.vs1, off, p);
+    else
+      put_k_row(staging_addr(s, w, layer, rec), tk.k + tok * tk.ks0 + h * tk.ks1, off, p);
+  }
+  if (!start) return;
+  const int bit = __builtin_ctzll(start);  // at most one slab starts among 16 tokens
+  const int64_t ssl = __shfl(sl, bit, 64);
+  const int b = (int)(ssl >> 7), st = (int)((ssl & 127) >> 4);
+  if (b >= s.NB) return;
+  const int w = s.wslot[b];
+  if (w < 0) return;
+  const int tok0 = t0 - kSlab + bit;
+  const int lrow = lane >> 4, lcol = (lane & 15) * 16;  // load: 16 lanes per 256-byte row
+  // chunk ci = lane + 64 m of the slab's 256: k = ci & 31 and half = ci >> 5
+  const int k = lane & 31, g = k >> 2, c = k & 3;
+  const uint16_t* src = is_v ? tk.v + tok0 * tk.vs0 + h * tk.vs1 : tk.k + tok0 * tk.ks0 + h * tk.ks1;
+  const int64_t rs = is_v ? tk.vs0 : tk.ks0;
+  uint4 row[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    row[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(src + (lrow + 4 * i) * rs) + lcol);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(lds + (lrow + 4 * i) * kSlabRow + lcol) = row[i];
+  wave_lds_sync();
+  uint8_t* dst = staging_addr(s, w, layer, rec);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int half = (lane >> 5) + 2 * m;  // K: dim slab st'; V: dim group tw
+    uint32_t q[4];
+    if (!is_v) {
+      // K chunk (st', t = 32 st + 4 g + c): u32 (2 j + f) = token 8 j + g, dims 16 st' + 8 f + 2 c, +1
+#pragma unroll
+      for (int jf = 0; jf < 4; ++jf)
+        q[jf] = *reinterpret_cast<const uint32_t*>(lds + (8 * (jf >> 1) + g) * kSlabRow +
+                                                   2 * (16 * half + 8 * (jf & 1) + 2 * c));
+      *reinterpret_cast<uint4*>(dst + 16 * (256 * half + 32 * st + k)) = make_uint4(q[0], q[1], q[2], q[3]);
+    } else {
+      // V chunk (st, t = 32 tw + 4 g + c): u16 (4 j + 2 f + e) = token 8 f + 2 c + e, dim 16 tw + 8 j + g
+#pragma unroll
+      for (int jf = 0; jf < 4; ++jf) {
+        const int j = jf >> 1, f = jf & 1, d = 16 * half + 8 * j + g;
+        const uint32_t lo = *reinterpret_cast<const uint16_t*>(lds + (8 * f + 2 * c) * kSlabRow + 2 * d);
+        const uint32_t hi = *reinterpret_cast<const uint16_t*>(lds + (8 * f + 2 * c + 1) * kSlabRow + 2 * d);
+        q[jf] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(dst + 16 * (256 * st + 32 * half + k)) = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
 }
 
 // The fused write + encode's encoder side: before a workgroup reads record
@@ -1366,8 +1487,8 @@ static int write_args(const fp_store_t* d, const void* key, int64_t k_s0, int64_
   tk = StepTokens{static_cast<const uint16_t*>(key), static_cast<const uint16_t*>(value), k_s0, k_s1, v_s0, v_s1,
                   slot_mapping, (int)n, 0};
   const int64_t items = n * d->kv_heads;
+  FP_CHECK(items < (1LL << 30), "too many (token, head) items in one step");  // int item indices
   write_grid = (items + kThreads / 64 - 1) / (kThreads / 64);
-  FP_CHECK(write_grid < (1LL << 30), "too many tokens");
   return 0;
 }
 
@@ -1380,7 +1501,18 @@ extern "C" int fp_hbm_write(const fp_store_t* d, const void* key, int64_t k_s0, 
   int64_t grid = 0;
   if (write_args(d, key, k_s0, k_s1, value, v_s0, v_s1, slot_mapping, n, layer, tk, grid)) return -1;
   const Store s = make_store(d);
-  hipLaunchKernelGGL(write_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, tk, (int)layer);
+  // Large steps with 16-byte aligned K and V rows take the slab path: one
+  // wave per 16 tokens and record.  Either grid is a multiple of 8 (XCD-contiguous).
+  const bool aligned = ((reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value)) & 15) == 0 &&
+                       ((k_s0 | k_s1 | v_s0 | v_s1) & 7) == 0;
+  if (n * d->kv_heads >= kWriteSlabItems && aligned) {
+    grid = ((n + kSlab - 1) / kSlab * 2 * d->kv_heads + kThreads / 64 - 1) / (kThreads / 64);
+    grid = (grid + kXcds - 1) / kXcds * kXcds;
+    hipLaunchKernelGGL(write_slab_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, tk, (int)layer);
+  } else {
+    grid = (grid + kXcds - 1) / kXcds * kXcds;
+    hipLaunchKernelGGL(write_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, s, tk, (int)layer);
+  }
   FP_LAUNCH_CHECK();
   return 0;
 }

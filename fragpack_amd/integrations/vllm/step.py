@@ -242,6 +242,9 @@ class FragPackRunner:
         max_model_len: Longest sequence (sizes the prefill workspace).
         overflow_records: Raw-record overflow pool size.
         layer_names: Engine layer names in layer order (optional).
+        workspace_pages: Pages of the BF16 prefill workspace (default: a
+            step's whole token budget of fresh prompts, plus one partial
+            page per request, and at least one ``max_model_len`` context).
 
     Used from the model-runner thread only; every method enqueues on the
     current stream.
@@ -257,6 +260,7 @@ class FragPackRunner:
         max_model_len: int,
         overflow_records: int = OVERFLOW_RECORDS,
         layer_names: list[str] | None = None,
+        workspace_pages: int | None = None,
     ) -> None:
         import torch
 
@@ -277,7 +281,17 @@ class FragPackRunner:
             torch.empty(ml, dtype=torch.float32, device=self.device),
             torch.empty(plan, dtype=torch.int32, device=self.device),
         )
-        self.workspace_pages = -(-max_model_len // BLOCK_TOKENS)
+        # The reference sizes its workspace for one max-length context
+        # (backend.py:398-411), so a step of several fresh prompts prefills
+        # in one launch per pass.  Here one pass also holds a whole step of
+        # fresh prompts (the token budget plus a partial page per request):
+        # the step's prefill is then one launch, and the workspace stays a
+        # small fraction of the GPU's HBM.
+        if workspace_pages is None:
+            workspace_pages = max(-(-max_model_len // BLOCK_TOKENS), -(-max_tokens // BLOCK_TOKENS) + max_reqs)
+        if workspace_pages < -(-max_model_len // BLOCK_TOKENS):
+            raise ValueError(f"workspace of {workspace_pages} pages cannot hold a {max_model_len}-token context")
+        self.workspace_pages = workspace_pages
         shape = (self.workspace_pages, BLOCK_TOKENS, kv_heads, HEAD_DIM)
         self.wk = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
         self.wv = torch.empty(shape, dtype=torch.bfloat16, device=self.device)

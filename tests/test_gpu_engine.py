@@ -36,7 +36,7 @@ ATOL, RTOL = 2e-2, 1e-2
 T, D = 128, 128
 L, H, G = 3, 2, 4
 NB = 48
-MAX_LEN = 1024  # prefill workspace of 8 pages: two long prefills need two passes
+MAX_LEN = 1024  # the core driver keeps an 8-page prefill workspace: two long prefills need two passes
 MAX_TOKENS = 2048
 MAX_REQS = 8
 WIDTH = MAX_LEN // T
@@ -83,7 +83,7 @@ class Engine:
 
             self.tracker = OpenBlocks(T)
             self.runner = FragPackRunner(H, device_tables(tables, self.dev), self.dev, MAX_TOKENS, MAX_REQS,
-                                         MAX_LEN, overflow_records=64)
+                                         MAX_LEN, overflow_records=64, workspace_pages=WIDTH)
         else:
             self.fakes = fake_vllm.install(monkeypatch)
             path = tmp_path / "tables.npz"

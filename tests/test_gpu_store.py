@@ -47,7 +47,7 @@ class SimEngine:
     ``ordered``: records are placed in (kv, head) order."""
 
     def __init__(self, seed, layers=2, heads=2, blocks=12, page=None, staging=3, overflow=16, noisy=(),
-                 fused=False, ordered=False):
+                 fused=False, ordered=False, max_tokens=1024):
         import torch
 
         from fragpack_amd.compression.attn_tables import calibrate, device_tables
@@ -61,7 +61,7 @@ class SimEngine:
         # an engine's cache starts as garbage
         self.caches = [torch.randint(0, 256, (blocks, self.page), dtype=torch.uint8, device="cuda")
                        for _ in range(layers)]
-        self.max_tokens = 1024
+        self.max_tokens = max_tokens
         self.store = HbmKvStore(self.caches, heads, device_tables(self.table, torch.device("cuda")),
                                 max_tokens=self.max_tokens, staging_slots=staging, overflow_records=overflow)
         self.model = StoreModel(layers, blocks, heads, staging, self.store.scratch.shape[0],
@@ -86,8 +86,10 @@ class SimEngine:
         for b in blocks:
             self.filled.pop(b, None)
 
-    def step(self, sched):
-        """``sched``: (request, tokens) pairs; unknown requests are admitted."""
+    def step(self, sched, pad=0):
+        """``sched``: (request, tokens) pairs; unknown requests are admitted.
+        ``pad``: slots of -1 (an engine's padding tokens) follow every
+        ``pad``-th token of the GPU store's slot mapping."""
         import torch
 
         live = []
@@ -105,8 +107,12 @@ class SimEngine:
                 pos.append((blocks[p // T], p % T))
             closes += (computed + n) // T - computed // T
             self.reqs[name][1] = computed + n
-        slot_t = torch.tensor(slots, dtype=torch.int64, device="cuda")
-        self.store.prepare(slot_t, len(slots), np.array(live, np.int32))
+        dev_slots = slots
+        if pad:
+            dev_slots = [x for i, sl in enumerate(slots) for x in ((sl, -1) if i % pad == 0 else (sl,))]
+        real = np.array(dev_slots) >= 0
+        slot_t = torch.tensor(dev_slots, dtype=torch.int64, device="cuda")
+        self.store.prepare(slot_t, len(dev_slots), np.array(live, np.int32))
         self.model.prepare(slots, live)
         self.heirs_seen += len(self.model.heirs)
         self.check_bookkeeping(claims=True)
@@ -123,9 +129,10 @@ class SimEngine:
                     kv[k, hit, h] = kvgen.bf16_bits(mag * self.rng.choice([-1.0, 1.0], mag.shape))
             self.kv[layer, :, blk, off] = kv.transpose(1, 0, 2, 3)
             # K / V as strided views of a fused qkv row, as an engine hands them over
-            qkv = torch.empty(n, 3 * self.H, D, dtype=torch.bfloat16, device="cuda")
-            qkv[:, self.H : 2 * self.H] = _dev_bits(kv[0])
-            qkv[:, 2 * self.H :] = _dev_bits(kv[1])
+            qkv = torch.randn(len(dev_slots), 3 * self.H, D, device="cuda").to(torch.bfloat16)
+            rows = torch.from_numpy(np.flatnonzero(real)).cuda()
+            qkv[rows, self.H : 2 * self.H] = _dev_bits(kv[0])
+            qkv[rows, 2 * self.H :] = _dev_bits(kv[1])
             key, value = qkv[:, self.H : 2 * self.H], qkv[:, 2 * self.H :]
             if self.fused:
                 self.store.write_encode(layer, key, value, slot_t, closes, ordered=self.ordered)
@@ -521,3 +528,19 @@ def test_fused_write_encode_degenerate_steps():
     # block 1: rows 0..4 from step 1, row 5 from step 2
     want_k1 = torch.cat((kv[0, 101:106], kv[0, 228:229]))
     assert torch.equal(got[1][0][1, :6], want_k1.view(torch.int16))
+
+
+def test_large_step_writes_batched_items():
+    """Steps of 16,384+ (token, head) items take the write's slab path:
+    whole 16-token slabs leave as 16-byte chunks, the rest per token.  The
+    first step's padding slots (-1 after every 37th token) leave slabs
+    partly written; the second step's decodes put the prompt's tokens at
+    odd step offsets.  Records vs the oracle, open blocks' rows through a
+    gather, bookkeeping vs the store model."""
+    eng = SimEngine(7, layers=1, heads=8, blocks=48, staging=6, overflow=64, max_tokens=4096)
+    eng.step([("a", 1100), ("b", 935), ("c", 300)], pad=37)
+    eng.step([("a", 1), ("b", 1), ("c", 2000)])
+    closed = [b for b, f in eng.filled.items() if f == T]
+    assert len(closed) >= 20
+    eng.check_records(closed)
+    eng.check_gather()
