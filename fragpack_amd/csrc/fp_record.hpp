@@ -346,30 +346,44 @@ __device__ __forceinline__ void stage_escapes(Rd4&& rd4, const SlabHdr& h, const
 // (byte 7 = 0).  Scalar order within a word: natural (dwords hold scalars
 // 0,1 | 2,3 | 4,5 | 6,7) or, with kEvenOdd, (0,2 | 1,3 | 4,6 | 5,7), which
 // takes two byte permutes fewer (the attention kernel's tiles follow it).
+//
+// Per word: the high bytes come from the primary table by code, escapes
+// (code 7) from the next 8 bytes of the expanded escape stream at this
+// thread's running byte position (three aligned dword reads and two byte
+// alignments: one unaligned 8-byte LDS read measured slower); the escape
+// of scalar i takes stream byte rank(i), the number of escapes among
+// scalars < i.
 template <bool kEvenOdd = false, typename Emit>
 __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* esc, int eo, uint32_t lut0,
                                              uint32_t lut1, Emit&& emit) {
+  // 0x0C0C0C0C in an SGPR, so each selector below is one v_bitop3 (a
+  // literal operand would cost a separate v_xor)
+  uint32_t c0c;
+  asm("s_mov_b32 %0, 0x0c0c0c0c" : "=s"(c0c));
   static_for<0, 8>([&](auto st_c) {
     constexpr int st = decltype(st_c)::value;
     const uint32_t sk = sym_word(b, st);
     const uint32_t b8 = (sk + 0x11111111u) & 0x88888888u;  // bit 3 of each escape nibble
-    const uint32_t eb = b8 >> 3;
+    const uint32_t s_ev = sk & 0x07070707u, s_od = (sk >> 4) & 0x07070707u;
     // primary high bytes of scalars 0,2,4,6 / 1,3,5,7 (escape code 7 -> 0)
-    const uint32_t hp_ev = perm(lut1, lut0, sk & 0x07070707u);
-    const uint32_t hp_od = perm(lut1, lut0, (sk >> 4) & 0x07070707u);
-    // escape window: the next 8 bytes of the expanded escape stream
+    const uint32_t hp_ev = perm(lut1, lut0, s_ev);
+    const uint32_t hp_od = perm(lut1, lut0, s_od);
     const int a = eo & ~3;
     const uint32_t* ew = reinterpret_cast<const uint32_t*>(esc + a);
     const uint32_t d0 = ew[0], d1 = ew[1], d2 = ew[2];
     // v_alignbyte_b32 shifts by 8 x bits [1:0] of its last operand: eo as is
-    const uint32_t elo = alignbyte(d1, d0, (uint32_t)eo), ehi = alignbyte(d2, d1, (uint32_t)eo);
-    eo += __builtin_popcount(eb);
-    // selector nibble: exclusive escape rank for escapes, 0xC (-> 0x00) else
-    const uint32_t rank = eb * 0x11111110u;
-    const uint32_t m15 = b8 | (b8 - eb);  // 0xF in escape nibbles (no multiply)
-    const uint32_t sel = (rank & m15) | (~m15 & 0xCCCCCCCCu);
-    const uint32_t h_ev = hp_ev | perm(ehi, elo, sel & 0x0F0F0F0Fu);
-    const uint32_t h_od = hp_od | perm(ehi, elo, (sel >> 4) & 0x0F0F0F0Fu);
+    const uint2 win = make_uint2(alignbyte(d1, d0, (uint32_t)eo), alignbyte(d2, d1, (uint32_t)eo));
+    eo += __builtin_popcount(b8);
+    // nibble i of rank: escapes among nibbles < i (b8 = 8 x the escape bits)
+    const uint32_t rank = b8 * 0x02222222u;
+    // selector byte per scalar: its rank for an escape, 0x0C (-> byte 0x00)
+    // otherwise; the code-indexed mask is 0xF0 for an escape (keeping the
+    // scalar's rank nibble, the low one of the byte), 0xFF otherwise
+    const uint32_t m_ev = perm(0xF0FFFFFFu, 0xFFFFFFFFu, s_ev), m_od = perm(0xF0FFFFFFu, 0xFFFFFFFFu, s_od);
+    const uint32_t sel_ev = (rank & ~m_ev) | (c0c & m_ev);
+    const uint32_t sel_od = ((rank >> 4) & ~m_od) | (c0c & m_od);
+    const uint32_t h_ev = hp_ev | perm(win.y, win.x, sel_ev);
+    const uint32_t h_od = hp_od | perm(win.y, win.x, sel_od);
     const uint4 lw = b.v[st >> 1];
     const uint32_t la = (st & 1) ? lw.z : lw.x, lb = (st & 1) ? lw.w : lw.y;  // low bytes of 0..3 / 4..7
     if constexpr (kEvenOdd) {
