@@ -147,6 +147,19 @@ def plan_step(
     return HostStep(num_reqs, nd, num_tokens, closes, max_close, prefills)
 
 
+def default_workspace_pages(max_model_len: int, max_tokens: int, max_reqs: int) -> int:
+    """Pages of the BF16 prefill workspace: one max-length context, or a
+    whole step of fresh prompts if that is more (every token of the step's
+    budget plus one partial page per request).
+
+    The reference sizes the workspace for one max-length context
+    (backend.py:398-411), so a step of several fresh prompts prefills in one
+    launch per workspace pass; sized for the step, the step's prefill is one
+    launch, and the workspace stays a small fraction of the GPU's HBM.
+    """
+    return max(-(-max_model_len // BLOCK_TOKENS), -(-max_tokens // BLOCK_TOKENS) + max_reqs)
+
+
 def prefill_groups(
     qsl: NDArray[np.int64], seq: NDArray[np.int64], first: int, workspace_pages: int
 ) -> list[HostPrefillGroup]:
@@ -281,14 +294,8 @@ class FragPackRunner:
             torch.empty(ml, dtype=torch.float32, device=self.device),
             torch.empty(plan, dtype=torch.int32, device=self.device),
         )
-        # The reference sizes its workspace for one max-length context
-        # (backend.py:398-411), so a step of several fresh prompts prefills
-        # in one launch per pass.  Here one pass also holds a whole step of
-        # fresh prompts (the token budget plus a partial page per request):
-        # the step's prefill is then one launch, and the workspace stays a
-        # small fraction of the GPU's HBM.
         if workspace_pages is None:
-            workspace_pages = max(-(-max_model_len // BLOCK_TOKENS), -(-max_tokens // BLOCK_TOKENS) + max_reqs)
+            workspace_pages = default_workspace_pages(max_model_len, max_tokens, max_reqs)
         if workspace_pages < -(-max_model_len // BLOCK_TOKENS):
             raise ValueError(f"workspace of {workspace_pages} pages cannot hold a {max_model_len}-token context")
         self.workspace_pages = workspace_pages
@@ -477,6 +484,7 @@ __all__ = [
     "HostPrefillGroup",
     "HostStep",
     "PrefillGroup",
+    "default_workspace_pages",
     "layer_forward",
     "plan_step",
     "prefill_groups",

@@ -287,6 +287,30 @@ def test_prefill_groups_pack_rows_in_order_within_the_workspace():
             assert sorted(used) == list(range(len(g.src_rows)))
 
 
+def test_default_workspace_holds_a_step_of_fresh_prompts_in_one_group():
+    from fragpack_amd.integrations.vllm.step import default_workspace_pages, plan_step
+
+    rng = np.random.default_rng(9)
+    for _ in range(200):
+        max_len = int(rng.integers(1, 40)) * 100
+        max_tokens, max_reqs = int(rng.integers(1, 9000)), int(rng.integers(1, 40))
+        ws = default_workspace_pages(max_len, max_tokens, max_reqs)
+        assert ws >= -(-max_len // 128)
+        # fresh prompts (context = query, at least 2 tokens: 1 is a decode) within the
+        # step budget, request count and model length
+        R = int(rng.integers(1, max_reqs + 1))
+        qlen = rng.integers(2, min(max_len, max(max_tokens // R, 2)) + 1, R)
+        qlen = qlen[np.cumsum(qlen) <= max_tokens]
+        if qlen.size == 0:
+            continue
+        qsl = np.concatenate(([0], np.cumsum(qlen)))
+        hs = plan_step(qsl, qlen, int(qsl[-1]), ws, max_tokens)
+        assert len(hs.prefills) == 1 and (hs.prefills[0].r0, hs.prefills[0].r1) == (0, qlen.size)
+    # one max-length context always fits
+    assert default_workspace_pages(8192, 512, 4) == 64
+    assert default_workspace_pages(8320, 32768, 4) == 256 + 4
+
+
 def test_prefill_longer_than_the_workspace_is_rejected():
     from fragpack_amd.integrations.vllm.step import plan_step
 
