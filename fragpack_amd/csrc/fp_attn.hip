@@ -437,14 +437,30 @@ struct InlinePlan {
   int ppc, used;           // uniform
 };
 
+// One step of a wavefront prefix minimum of u64 keys by DPP: both halves
+// move with the same control; lanes without a source (shifted in, or rows
+// masked off) read all ones, the identity.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint64_t dpp_min_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)x, kCtrl, kRowMask, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)(x >> 32), kCtrl, kRowMask, 0xf, false);
+  const uint64_t y = ((uint64_t)hi << 32) | lo;
+  return y < x ? y : x;
+}
+
+// Minimum over the wavefront (uniform), by a DPP prefix scan (row shifts,
+// then row broadcasts; lane 63 ends with the minimum): VALU only, where a
+// butterfly of lane shuffles costs an LDS round trip per step.
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)x, o, 64), hi = __shfl_xor((uint32_t)(x >> 32), o, 64);
-    const uint64_t y = ((uint64_t)hi << 32) | lo;
-    x = y < x ? y : x;
-  }
-  return x;
+  x = dpp_min_u64<0x111, 0xf>(x);  // row_shr:1
+  x = dpp_min_u64<0x112, 0xf>(x);  // row_shr:2
+  x = dpp_min_u64<0x114, 0xf>(x);  // row_shr:4
+  x = dpp_min_u64<0x118, 0xf>(x);  // row_shr:8
+  x = dpp_min_u64<0x142, 0xa>(x);  // row_bcast:15
+  x = dpp_min_u64<0x143, 0xc>(x);  // row_bcast:31
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(x >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane) {
