@@ -530,16 +530,18 @@ def test_fused_write_encode_degenerate_steps():
     assert torch.equal(got[1][0][1, :6], want_k1.view(torch.int16))
 
 
-def test_large_step_writes_batched_items():
+@pytest.mark.parametrize("heads", [8, 2])
+def test_large_step_writes_batched_items(heads):
     """Steps of 16,384+ (token, head) items take the write's slab path:
     whole 16-token slabs leave as 16-byte chunks, the rest per token.  The
     first step's padding slots (-1 after every 37th token) leave slabs
     partly written; the second step's decodes put the prompt's tokens at
     odd step offsets.  Records vs the oracle, open blocks' rows through a
     gather, bookkeeping vs the store model."""
-    eng = SimEngine(7, layers=1, heads=8, blocks=48, staging=6, overflow=64, max_tokens=4096)
-    eng.step([("a", 1100), ("b", 935), ("c", 300)], pad=37)
-    eng.step([("a", 1), ("b", 1), ("c", 2000)])
+    k = 8 // heads  # the same number of (token, head) items at either head count
+    eng = SimEngine(7, layers=1, heads=heads, blocks=48 * k, staging=6, overflow=64 * k, max_tokens=4096 * k)
+    eng.step([("a", 1100 * k), ("b", 935 * k), ("c", 300 * k)], pad=37)
+    eng.step([("a", 1), ("b", 1), ("c", 2000 * k)])
     closed = [b for b, f in eng.filled.items() if f == T]
     assert len(closed) >= 20
     eng.check_records(closed)
