@@ -546,3 +546,53 @@ def test_large_step_writes_batched_items(heads):
     assert len(closed) >= 20
     eng.check_records(closed)
     eng.check_gather()
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_random_serving_steps(fused):
+    """Forty random serving steps: requests arrive with prompts of 2..4000
+    tokens, prefill in chunks of up to 3000 tokens, then decode one token a
+    step and finish at random; some steps carry padding slots, and steps of
+    4096+ tokens take the slab write (or, fused, the one-launch write +
+    encode at that size).  Bookkeeping equals the store model
+    after every prepare and commit; at the end every closed block's records
+    equal the oracle codec's and every written row gathers back."""
+    import torch
+
+    rng = np.random.default_rng(1234 + fused)
+    eng = SimEngine(41, layers=1, heads=4, blocks=240, staging=8, overflow=256, fused=fused, max_tokens=8192)
+    prompt: dict[str, int] = {}  # request -> prompt tokens not yet scheduled
+    admitted, large_steps = 0, 0
+    for step in range(40):
+        while len(prompt) < 6 and rng.random() < 0.7:
+            prompt[f"r{admitted}"] = int(rng.integers(2, 4000))
+            admitted += 1
+        free = len(eng.pool)
+        sched, tokens = [], 0
+        for name, rem in prompt.items():
+            blocks, computed = eng.reqs.get(name, [[], 0])
+            n = min(rem, int(rng.integers(1, 3000)), 7500 - tokens) if rem else 1
+            n = max(n, 0)
+            while n > 0 and -(-(computed + n) // T) - len(blocks) > free:
+                n //= 2
+            if n == 0:
+                continue
+            free -= -(-(computed + n) // T) - len(blocks)
+            sched.append((name, n))
+            tokens += n
+        if not sched:
+            continue
+        large_steps += tokens * eng.H >= 1 << 14
+        eng.step(sched, pad=int(rng.integers(20, 60)) if rng.random() < 0.3 else 0)
+        for name, n in sched:
+            prompt[name] = max(prompt[name] - n, 0) if prompt[name] else 0
+        for name in [r for r, rem in prompt.items() if rem == 0 and r in eng.reqs and rng.random() < 0.25]:
+            eng.finish(name)
+            del prompt[name]
+    assert large_steps >= 3
+    torch.cuda.synchronize()
+    st = eng.store.stats()
+    assert (st.err_staging, st.err_overflow) == (0, 0)
+    closed = sorted(b for b, n in eng.filled.items() if n == T)
+    eng.check_records(closed)
+    eng.check_gather()
