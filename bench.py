@@ -15,8 +15,14 @@ BF16-KV throughput (2 * sum(ceil(len/128)) * 128 * H * 128 * 2 bytes per
 step / step time), the reference benchmark's convention
 (benchmarks/fragpack_step_bench.py:320).  Extra fields report us/step, the
 compressed-byte rate, the roofline of the attention kernel (algorithmic
-compressed bytes per launch / its HIP-event time), the encoder leg (BASELINE
-config 3 shape) and the CPU oracle baseline.
+compressed bytes per launch / its HIP-event time) and the CPU oracle
+baseline, then one field per leg (each switched off by its ``--no-*`` flag):
+the BF16 paged arm and the all-raw-record arm at config 1; config 4 decode
+(``decode_large``) and the B64 context sweep; config 2 (MHA, ragged); the
+config-4 prefill; the encoder at config 3's shape; the other store kernels;
+the layer step (prepare / write / attention / encode, separate and fused);
+config 4 through the serving step protocol; the device's plain read / copy /
+fill rates.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
