@@ -147,3 +147,27 @@ def test_c_abi_rejects_bad_arguments_without_gpu_work():
     # empty batch is a no-op
     assert f(None, 4096, 0, 4, 8, None, None, None, None, None, 1, None, None, 0, None, 0, None, 0, None, 4096, 0, 1,
              0.1, None) == 0
+
+
+def test_store_write_rejects_bad_steps_without_gpu_work():
+    """The store write's argument checks (fp_store.hip write_args) return -1
+    with a message before any launch: a step of 2^30+ (token, head) items,
+    odd strides; an empty step is a no-op."""
+    from fragpack_amd.ops.fragpack_ext import FpStore
+
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.fp_last_error.restype = ctypes.c_char_p
+    f = lib.fp_hbm_write
+    f.restype = ctypes.c_int
+    p, i64 = ctypes.c_void_p, ctypes.c_int64
+    f.argtypes = [ctypes.POINTER(FpStore), p, i64, i64, p, i64, i64, p, i64, i64, p]
+    d = FpStore(num_layers=1, num_blocks=4, kv_heads=8, staging_slots=2, scratch_slots=2, ovf_words=1, list_cap=64,
+                overflow_records=32)
+    dummy = p(256)  # never dereferenced: the checks fail first
+    rc = f(ctypes.byref(d), dummy, 8 * 128, 128, dummy, 8 * 128, 128, dummy, 1 << 27, 0, None)
+    assert rc == -1 and b"items" in lib.fp_last_error()
+    rc = f(ctypes.byref(d), dummy, 8 * 128 + 1, 128, dummy, 8 * 128, 128, dummy, 16, 0, None)
+    assert rc == -1 and b"strides" in lib.fp_last_error()
+    rc = f(ctypes.byref(d), dummy, 8 * 128, 128, dummy, 8 * 128, 128, dummy, 16, 5, None)
+    assert rc == -1 and b"layer" in lib.fp_last_error()
+    assert f(ctypes.byref(d), dummy, 8 * 128, 128, dummy, 8 * 128, 128, dummy, 0, 0, None) == 0
