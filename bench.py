@@ -19,7 +19,7 @@ compressed bytes per launch / its HIP-event time) and the CPU oracle
 baseline, then one field per leg (each switched off by its ``--no-*`` flag):
 the BF16 paged arm and the all-raw-record arm at config 1; config 4 decode
 (``decode_large``) and the B64 context sweep; config 2 (MHA, ragged); the
-config-4 prefill; the encoder at config 3's shape; the other store kernels;
+config-4 prefill and a chunked prefill over the same contexts; the encoder at config 3's shape; the other store kernels;
 the layer step (prepare / write / attention / encode, separate and fused);
 config 4 through the serving step protocol; the device's plain read / copy /
 fill rates.
@@ -487,15 +487,20 @@ def pipeline_bench(torch, args) -> dict:
     return res
 
 
-def prefill_bench(torch, args) -> dict:
-    """Causal prefill over config 4's prompts: ``--prefill-seqs`` x
+def prefill_bench(torch, args, qlen: int | None = None) -> dict:
+    """Causal prefill over config 4's prompts: ``--prefill-seqs`` contexts of
     ``--prefill-len`` tokens, 32 query heads over 8 KV heads (GQA 4), on a
-    paged BF16 workspace (pages in permuted order).  FLOPs = 4 * D * Hq *
-    sum over queries of the keys it sees (QK^T and PV, 2 flops per MAC).
-    Checked against an fp32 reference on a sample of query rows."""
+    paged BF16 workspace (pages in permuted order).  ``qlen``: new tokens per
+    sequence, the last ``qlen`` positions of each context (a chunked prefill
+    over cached context, causal aligned bottom-right); default: the whole
+    prompt.  FLOPs = 4 * D * Hq * sum over queries of the keys it sees (QK^T
+    and PV, 2 flops per MAC).  Checked against an fp32 reference on a sample
+    of query rows."""
     from fragpack_amd.ops.prefill_attn import flash_attn_varlen_func
 
     S, L, H, G = args.prefill_seqs, args.prefill_len, 8, 4
+    Q = qlen or L
+    shift = L - Q  # query row r sees keys <= r + shift
     gen = torch.Generator(device="cuda").manual_seed(args.seed + 4)
     pages_per = math.ceil(L / T)
     n_pages = S * pages_per
@@ -503,25 +508,25 @@ def prefill_bench(torch, args) -> dict:
     bt = torch.from_numpy(rng.permutation(n_pages).astype(np.int32).reshape(S, pages_per)).cuda()
     wk = torch.randn((n_pages, T, H, D), generator=gen, device="cuda").to(torch.bfloat16)
     wv = torch.randn((n_pages, T, H, D), generator=gen, device="cuda").to(torch.bfloat16)
-    q = torch.randn((S * L, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
+    q = torch.randn((S * Q, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
     out = torch.empty_like(q)
-    cu = torch.arange(0, S * L + 1, L, dtype=torch.int32, device="cuda")
+    cu = torch.arange(0, S * Q + 1, Q, dtype=torch.int32, device="cuda")
     kl = torch.full((S,), L, dtype=torch.int32, device="cuda")
     scale = D ** -0.5
 
     def run():
-        flash_attn_varlen_func(q=q, k=wk, v=wv, out=out, cu_seqlens_q=cu, max_seqlen_q=L, seqused_k=kl,
+        flash_attn_varlen_func(q=q, k=wk, v=wv, out=out, cu_seqlens_q=cu, max_seqlen_q=Q, seqused_k=kl,
                                max_seqlen_k=L, softmax_scale=scale, causal=True, block_table=bt)
 
     run()
     torch.cuda.synchronize()
     # fp32 reference on sampled query rows of sequence 0
-    rows = torch.from_numpy(np.sort(rng.choice(L, size=min(L, 48), replace=False))).cuda()
+    rows = torch.from_numpy(np.sort(rng.choice(Q, size=min(Q, 48), replace=False))).cuda()
     pg = bt[0].long()
     k0 = wk[pg].reshape(-1, H, D)[:L].float().repeat_interleave(G, dim=1)  # [L, Hq, D]
     v0 = wv[pg].reshape(-1, H, D)[:L].float().repeat_interleave(G, dim=1)
     s = torch.einsum("rhd,khd->hrk", q[rows].float(), k0) * scale
-    s = s.masked_fill(torch.arange(L, device="cuda")[None, None, :] > rows[None, :, None], float("-inf"))
+    s = s.masked_fill(torch.arange(L, device="cuda")[None, None, :] > rows[None, :, None] + shift, float("-inf"))
     ref = torch.einsum("hrk,khd->rhd", torch.softmax(s, -1), v0)
     err = (out[rows].float() - ref).abs()
     valid = bool(torch.isfinite(out.float()).all() and (err <= 2e-2 + 1e-2 * ref.abs()).all())
@@ -535,8 +540,8 @@ def prefill_bench(torch, args) -> dict:
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    flops = 4.0 * D * H * G * S * (L * (L + 1) / 2)
-    log(f"prefill {S}x{L} Hq{H * G}/H{H}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s, sampled max err "
+    flops = 4.0 * D * H * G * S * (Q * shift + Q * (Q + 1) / 2)
+    log(f"prefill {S}x{Q} new over {L} Hq{H * G}/H{H}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s, sampled max err "
         f"{err.max().item():.3e}, valid {valid}")
     return dict(ms=ms, flops=flops, valid=valid, max_err=err.max().item())
 
@@ -911,6 +916,7 @@ def main() -> None:
     enc = None if args.no_encode else encode_bench(torch, args)
     enc_ordered = None if args.no_encode else encode_bench(torch, args, ordered=True)
     pre = None if args.no_prefill else prefill_bench(torch, args)
+    pre_chunk = None if args.no_prefill else prefill_bench(torch, args, qlen=args.prefill_len // 8)
     cpu = None if args.no_cpu else cpu_baseline(torch, res, args)
     paged = None if args.no_raw_arm else paged_bench(torch, args)
     raw = None
@@ -1030,6 +1036,13 @@ def main() -> None:
                            "tflops": round(tf, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                            "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "validated": pre["valid"],
                            "sampled_max_abs_err": pre["max_err"]}
+        if pre_chunk is not None:
+            tfc = pre_chunk["flops"] / (pre_chunk["ms"] / 1e3) / 1e12
+            line["prefill"]["chunked"] = {
+                "workload": f"{args.prefill_seqs} x {args.prefill_len // 8} new tokens over {args.prefill_len}-token "
+                            "contexts (chunked prefill, causal bottom-right)",
+                "ms": round(pre_chunk["ms"], 3), "tflops": round(tfc, 1),
+                "mfma_frac": round(tfc / MFMA_BF16_PEAK_TFLOPS, 4), "validated": pre_chunk["valid"]}
     if paged is not None:
         line["bf16_paged_arm"] = {
             "what": "the same step through the plain BF16 paged decode kernel (fp_paged_decode) over a "
