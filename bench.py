@@ -55,11 +55,26 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def rotations(args, eff_bytes_per_layer: int) -> int:
+    """Distinct layers a timed loop rotates over: enough that the records
+    read by consecutive launches (``--rotate-bytes``, default 768 MB) exceed
+    MI355X's 256 MB Infinity Cache, so each launch reads HBM as a serving
+    step does (every layer reads its own records); 1 for a layer already that
+    large."""
+    return max(1, math.ceil(args.rotate_bytes / eff_bytes_per_layer)) if args.rotate_bytes else 1
+
+
 def decode_bench(torch, args, raw: bool = False) -> dict:
     """One decode step (plan + attention) over a filled store.  ``raw``: the
-    BF16 paged baseline arm -- tables whose 22 high bytes never occur in the
+    all-raw-record arm -- tables whose 22 high bytes never occur in the
     data (0x00..0x15), so every record falls back to its raw 32 KB form and
-    the same kernel streams plain BF16 pages."""
+    the same kernel streams plain BF16 pages.
+
+    The store holds ``R = rotations(...)`` layers, each with KV of its own
+    under the same block table (as a model's layers are); the cold figures
+    rotate the timed launches over the layers, the warm ones repeat layer 0.
+    A replanning call plans on the layer it attends; a call that reuses the
+    plan reads the block ids the plan holds, valid for every layer."""
     from fragpack_amd.ops.fused_attn_decode import RecordTables, decode_attention, decode_units, workspace_elems
 
     B, H, G, ctx = args.batch, args.heads, args.group, args.context
@@ -68,15 +83,16 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
     tables = calibrated_tables(rng, H, scales)
     pages = math.ceil(ctx / T)
     nb = B * pages
-    overflow = 8192
+    R = rotations(args, 2 * nb * T * H * D * 2)
+    overflow = 8192 * R
     if raw:
         tables = np.broadcast_to(np.arange(22, dtype=np.uint8), tables.shape).copy()
-        overflow = nb * 2 * H + 64
+        overflow = nb * 2 * H * R + 64
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
     scales_t = torch.from_numpy(scales).float().cuda()
     t0 = time.time()
     store, arena, kv = build_store(torch, H, nb, tables, gen, scales_t, fill_blocks=64, keep_kv=True,
-                                   overflow=overflow)
+                                   overflow=overflow, layers=R)
     log(f"store filled: {nb} blocks x {2 * H} records in {time.time() - t0:.1f}s, stats {store.stats()}")
     perm = torch.from_numpy(rng.permutation(nb).astype(np.int32)).cuda()
     bt = perm.view(B, pages).contiguous()
@@ -88,11 +104,17 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
     ws = (torch.empty(opart, device="cuda"), torch.empty(ml, device="cuda"),
           torch.empty(plan, dtype=torch.int32, device="cuda"))
     out = torch.empty_like(q)
-    tabs = RecordTables(*store.layer_tables(0))
+    tabs = [RecordTables(*store.layer_tables(r)) for r in range(R)]
     scale = D ** -0.5
 
-    def step(replan=True):
-        decode_attention(q, tabs, bt, lens, scale, units, out, ws, replan)
+    def step(replan=True, r=0):
+        decode_attention(q, tabs[r], bt, lens, scale, units, out, ws, replan)
+
+    turn = [0]
+
+    def step_cold(replan=True):
+        turn[0] = (turn[0] + 1) % R
+        step(replan, turn[0])
 
     # validation against an fp32 torch reference on the written KV
     out.fill_(float("nan"))
@@ -106,13 +128,16 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
     del kv
 
     # algorithmic bytes of one launch
-    rec_len = store.rec_len[0].cpu().numpy()  # [NB, 2, H]
+    # (the layers hold the same number of records; their coded sizes differ
+    # by a fraction of a percent, so the mean is used cold)
     used = bt.cpu().numpy()[:, :pages].reshape(-1)
-    rl = rec_len[used]  # [B*pages, 2, H]
-    rec_bytes = int(np.where(rl > 2048, 32768, DENSE + rl).sum())
+    rl_all = np.where(store.rec_len.cpu().numpy() > 2048, 32768, DENSE + store.rec_len.cpu().numpy())  # [L, NB, 2, H]
+    per_rot = [int(rl_all[r][used].sum()) for r in range(R)]
+    rec_bytes = per_rot[0]
     meta_bytes = used.size * H * 24
     qo_bytes = B * H * G * D * 2 * 2
     algo_bytes = rec_bytes + meta_bytes + qo_bytes
+    algo_cold = int(np.mean(per_rot)) + meta_bytes + qo_bytes
     eff_bytes = 2 * B * pages * T * H * D * 2
 
     stream = torch.cuda.current_stream()
@@ -140,25 +165,42 @@ def decode_bench(torch, args, raw: bool = False) -> dict:
     # the attention kernel alone (replan=False launches only attn_kernel);
     # both measured twice, interleaved, keeping the second of each (the
     # first timed region after the fp32 validation runs measurably slow)
+    # cold: each launch reads another layer's records (R > 1); warm: the
+    # same layer's records every launch (Infinity Cache hits)
     for _ in range(2):
-        step_ms = timed(step)
-        kern_ms = timed(lambda: step(False))
+        step_ms = timed(step_cold)
+        kern_ms = timed(lambda: step_cold(False))
+    warm_step_ms = warm_kern_ms = None
+    if R > 1:
+        for _ in range(2):
+            warm_step_ms = timed(step)
+            warm_kern_ms = timed(lambda: step(False))
     # the same step captured 16 times into one HIP graph (as a serving
-    # engine captures a decode step of many layers) and replayed; per step
+    # engine captures a decode step of many layers; the layers rotate) and
+    # replayed; per step
     graph_steps = 16
     side = torch.cuda.Stream()
     side.wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        for _ in range(graph_steps):
-            step(True)
+        for i in range(graph_steps):
+            step(True, i % R)
     graph.replay()
     graph_ms = timed(graph.replay) / graph_steps
     comp_ratio = rec_bytes / (2 * used.size * H * 32768)
-    log(f"step {step_ms * 1e3:.1f} us, attn kernel {kern_ms * 1e3:.1f} us, "
+    if R > 1:
+        # check the last rotated call (layer R - 1) too
+        out.fill_(float("nan"))
+        step(True, R - 1)
+        step(False, R - 1)
+        torch.cuda.synchronize()
+        valid = valid and bool(torch.isfinite(out.float()).all())
+    log(f"step {step_ms * 1e3:.1f} us, attn kernel {kern_ms * 1e3:.1f} us (rotating over {R} layers; warm "
+        f"{warm_step_ms and warm_step_ms * 1e3} / {warm_kern_ms and warm_kern_ms * 1e3} us), "
         f"compressed {rec_bytes / 1e6:.1f} MB ({comp_ratio:.3f} of raw), effective BF16 {eff_bytes / 1e6:.1f} MB")
-    return dict(step_ms=step_ms, kern_ms=kern_ms, graph_ms=graph_ms, algo_bytes=algo_bytes, eff_bytes=eff_bytes, rec_bytes=rec_bytes,
-                valid=valid, units=units, store=store, arena=arena, bt=bt, lens=lens, q=q, tables=tables,
+    return dict(step_ms=step_ms, kern_ms=kern_ms, graph_ms=graph_ms, algo_bytes=algo_cold, eff_bytes=eff_bytes,
+                rec_bytes=rec_bytes, warm_step_ms=warm_step_ms, warm_kern_ms=warm_kern_ms, warm_algo_bytes=algo_bytes,
+                rotations=R, valid=valid, units=units, store=store, arena=arena, bt=bt, lens=lens, q=q, tables=tables,
                 scale=scale, comp_ratio=comp_ratio, max_err=err.max().item())
 
 
@@ -176,9 +218,11 @@ def paged_bench(torch, args) -> dict:
     scales = channel_scales(rng, H, 0.02)
     gen = torch.Generator(device="cuda").manual_seed(args.seed + 11)
     pages = math.ceil(ctx / T)
-    nb = B * pages
+    R = rotations(args, 2 * B * pages * T * H * D * 2)
+    nb = B * pages * R
     kv = gen_kv(torch, gen, nb * T, H, torch.from_numpy(scales).float().cuda()).view(2, nb, T, H, D)
-    bt = torch.from_numpy(rng.permutation(nb).astype(np.int32)).cuda().view(B, pages).contiguous()
+    bts = torch.from_numpy(rng.permutation(nb).astype(np.int32)).cuda().view(R, B, pages).contiguous()
+    bt = bts[0]
     lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
     q = torch.randn((B, H * G, D), generator=gen, device="cuda").to(torch.bfloat16)
     out = torch.empty_like(q)
@@ -186,8 +230,14 @@ def paged_bench(torch, args) -> dict:
     ws = paged_workspace(B, H, splits, q.device)
     scale = D ** -0.5
 
-    def step():
-        paged_decode_attention(q, kv[0], kv[1], bt, lens, ctx, scale, out, ws, splits)
+    def step(r=0):
+        paged_decode_attention(q, kv[0], kv[1], bts[r], lens, ctx, scale, out, ws, splits)
+
+    turn = [0]
+
+    def step_cold():
+        turn[0] = (turn[0] + 1) % R
+        step(turn[0])
 
     out.fill_(float("nan"))
     step()
@@ -198,23 +248,30 @@ def paged_bench(torch, args) -> dict:
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream()
-    ms = []
-    for _ in range(2):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        torch.cuda._sleep(int(args.steps * 40_000))  # host enqueues while the GPU spins
-        e0.record(stream)
-        for _ in range(args.steps):
-            step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms.append(e0.elapsed_time(e1) / args.steps)
-    step_ms = ms[-1]
-    nbytes = 2 * nb * T * H * D * 2 + 2 * B * H * G * D * 2
-    log(f"BF16 paged arm B{B} H{H} G{G} {ctx}: {step_ms * 1e3:.1f} us/step ({nbytes / step_ms / 1e6:.0f} GB/s), "
-        f"splits {splits}, max err {err.max().item():.3e}, valid {valid}")
+
+    def timed(fn):
+        ms = []
+        for _ in range(2):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(args.steps * 40_000))  # host enqueues while the GPU spins
+            e0.record(stream)
+            for _ in range(args.steps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1) / args.steps)
+        return ms[-1]
+
+    step_ms = timed(step_cold)
+    warm_ms = timed(step) if R > 1 else None
+    nbytes = 2 * B * pages * T * H * D * 2 + 2 * B * H * G * D * 2
+    log(f"BF16 paged arm B{B} H{H} G{G} {ctx}: {step_ms * 1e3:.1f} us/step ({nbytes / step_ms / 1e6:.0f} GB/s) rotating "
+        f"over {R} layers, warm {warm_ms and warm_ms * 1e3} us; splits {splits}, max err {err.max().item():.3e}, "
+        f"valid {valid}")
     del kv
-    return dict(step_ms=step_ms, bytes=nbytes, valid=valid, splits=splits, max_err=err.max().item())
+    return dict(step_ms=step_ms, warm_step_ms=warm_ms, rotations=R, bytes=nbytes, valid=valid, splits=splits,
+                max_err=err.max().item())
 
 
 def _timed(torch, args, step) -> float:
@@ -313,6 +370,16 @@ def config2_bench(torch, args) -> dict:
         res[name].update(us_per_step=round(ms * 1e3, 2), effective_GBps=round(eff / ms / 1e6, 1))
     rl = store.rec_len[0].cpu().numpy()[perm]
     coded = int((rl <= 2048).sum())
+    # algorithmic bytes of the compressed launch (one planning attn_kernel):
+    # every page's K and V records (coded: DENSE + var, raw tails 32 KB),
+    # 24 B of record metadata per (page, head), Q and out
+    algo = int(np.where(rl > 2048, 32768, DENSE + rl).sum()) + nb * H * 24 + 2 * B * H * G * D * 2
+    ms_c = res["compressed"]["us_per_step"] / 1e3
+    prof = profiled_traffic("attn_kernel", "config2") or {}
+    res["compressed"]["roofline"] = {
+        "bound": "hbm", "kernel": "attn_kernel", "achieved": round(algo / ms_c / 1e6, 1), "peak": HBM_PEAK_GBS,
+        "unit": "GB/s", "frac": round(algo / ms_c / 1e6 / HBM_PEAK_GBS, 4),
+        "traffic": prof.get("traffic_bytes_per_launch"), "algo_bytes_per_launch": algo}
     res.update(workload="config 2: MHA decode, B16 x H32 x G1, ragged U[129, 4096], 5% outlier channels",
                lens_sum=n_tok, blocks=nb, coded_records=coded, records=int(rl.size),
                encoded=stats.encoded, fallbacks=stats.fallbacks,
@@ -816,6 +883,8 @@ def cpu_baseline(torch, res, args) -> dict:
     from oracle import oracle
 
     store, arena = res["store"], res["arena"]
+    if isinstance(arena, list):  # layer 0 of a rotation store
+        arena = arena[0]
     host_arena = arena.cpu().numpy().reshape(-1)
     host_ovf = store.overflow.cpu().numpy().reshape(-1)
     recs = np.concatenate([host_arena, host_ovf])
@@ -868,6 +937,8 @@ def main() -> None:
     ap.add_argument("--context", type=int, default=8192)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--units", type=int, default=0, help="override decode_units()")
+    ap.add_argument("--rotate-bytes", type=float, default=768e6,
+                    help="BF16-equivalent KV bytes the timed decode launches rotate over (0: one layer, warm)")
     ap.add_argument("--encode-blocks", type=int, default=32768)
     ap.add_argument("--encode-reps", type=int, default=3)
     ap.add_argument("--encode-heavy", type=float, default=0.1, help="Student-t(2) x 16 share of encode values")
@@ -1018,6 +1089,14 @@ def main() -> None:
         "config": {"workload": "config 1: decode step, B4 x H4 x G8 x 8192 ctx, head_dim 128, one layer",
                    "batch": args.batch, "kv_heads": args.heads, "gqa": args.group, "context": args.context,
                    "units": res["units"]},
+        "cache": (f"cold: the timed launches rotate over {res['rotations']} layers' records "
+                  f"({res['rotations'] * res['rec_bytes'] / 1e6:.0f} MB, above the 256 MB Infinity Cache)"
+                  if res["rotations"] > 1 else "one layer per launch"),
+        "warm": None if res["warm_step_ms"] is None else {
+            "what": "the same layer's records every launch (served partly from the Infinity Cache)",
+            "us_per_step": round(res["warm_step_ms"] * 1e3, 2), "kernel_us": round(res["warm_kern_ms"] * 1e3, 2),
+            "value": round(res["eff_bytes"] / (res["warm_step_ms"] / 1e3) / 1e9, 2),
+            "roofline_frac": round(res["warm_algo_bytes"] / (res["warm_kern_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)},
         "graph_us_per_step": round(res["graph_ms"] * 1e3, 2),
         "compressed_GBps": round(res["algo_bytes"] / step_s / 1e9, 2),
         "compression": round(res["comp_ratio"], 4),
@@ -1049,13 +1128,17 @@ def main() -> None:
                     "[blocks, 128, H, 128] cache (the reference benchmark's FA3 arm)",
             "us_per_step": round(paged["step_ms"] * 1e3, 2), "splits": paged["splits"], "validated": paged["valid"],
             "compressed_step_speedup": round(paged["step_ms"] / res["step_ms"], 3),
-            "hbm_GBps": round(paged["bytes"] / (paged["step_ms"] / 1e3) / 1e9, 1)}
+            "hbm_GBps": round(paged["bytes"] / (paged["step_ms"] / 1e3) / 1e9, 1),
+            "warm_us_per_step": paged["warm_step_ms"] and round(paged["warm_step_ms"] * 1e3, 2),
+            "warm_compressed_step_speedup": paged["warm_step_ms"] and res["warm_step_ms"] and
+            round(paged["warm_step_ms"] / res["warm_step_ms"], 3)}
     if raw is not None:
         line["all_raw_record_arm"] = {
             "what": "the FragPack kernel over all-raw records (every record 32 KB BF16 in kernel order)",
             "us_per_step": round(raw["step_ms"] * 1e3, 2), "kernel_us": round(raw["kern_ms"] * 1e3, 2),
             "validated": raw["valid"], "compressed_step_speedup": round(raw["step_ms"] / res["step_ms"], 3),
-            "hbm_GBps": round(raw["algo_bytes"] / (raw["kern_ms"] / 1e3) / 1e9, 1)}
+            "hbm_GBps": round(raw["algo_bytes"] / (raw["kern_ms"] / 1e3) / 1e9, 1),
+            "warm_us_per_step": raw["warm_step_ms"] and round(raw["warm_step_ms"] * 1e3, 2)}
     if large is not None:
         lk = large["kern_ms"] / 1e3
         la = large["algo_bytes"] / lk / 1e9
@@ -1099,7 +1182,14 @@ def main() -> None:
                                               "records the full pool dropped are excluded",
                           "hbm_GBps": round(enc["read_write_bytes"] / enc["ms"] / 1e6, 1),
                           "fallbacks": enc["fallbacks"], "spills": enc["spills"],
-                          "overflow_full_drops": enc["err_overflow"]}
+                          "overflow_full_drops": enc["err_overflow"],
+                          "roofline": {"bound": "hbm", "kernel": "encode_kernel",
+                                       "achieved": round(enc["read_write_bytes"] / enc["ms"] / 1e6, 1),
+                                       "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                       "frac": round(enc["read_write_bytes"] / enc["ms"] / 1e6 / HBM_PEAK_GBS, 4),
+                                       "traffic": (profiled_traffic("encode_kernel", "config3") or {}).get(
+                                           "traffic_bytes_per_launch"),
+                                       "algo_bytes_per_launch": enc["read_write_bytes"]}}
         if enc_ordered is not None:
             line["encode"]["ordered"] = {"what": "block-major encode placing each block's records in (kv, head) "
                                                  "order: the same spill set on every run",

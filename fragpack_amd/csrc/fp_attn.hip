@@ -76,15 +76,6 @@ struct AttnParams {
   int inline_plan;  // 1: every workgroup plans for itself (batch <= 64)
   int bt_lds;       // inline plan and the whole block table (batch x bt_stride <= kBtLds) read into LDS
   float scale_log2;
-  // Optional append of each sequence's new token (decode rows: position
-  // seq_len - 1) into its open block's raw record before attention reads it;
-  // null nk: no append.  Records are written only when they lie inside
-  // [w_lo0, w_hi0) or [w_lo1, w_hi1) (the store's staging and scratch).
-  const uint16_t* nk;
-  const uint16_t* nv;
-  const int64_t* new_slot;  // new token b goes to slot new_slot[b] (block * 128 + row); < 0: none
-  int64_t nk_s0, nk_s1, nv_s0, nv_s1;  // token / head strides (elements)
-  uint64_t w_lo0, w_hi0, w_lo1, w_hi1;
 };
 
 // Plan layout (int32): [0] ppc, [1] units in use, [2, 2 + 2 units) (sequence, first
@@ -486,48 +477,6 @@ __device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane)
   return r;
 }
 
-// The store's write (write_kernel in fp_store.hip) of sequence b's new token
-// for head h, done by the unit that owns the sequence's last page: the token
-// goes to its slot (block * 128 + row; a negative slot is padding), which for
-// a decode row is row (seq - 1) % 128 of that last page.
-// Each wave writes what its own slab holds -- the K token lies in slab
-// (row / 32), a V token spreads over all four slabs, 32 dims each -- so every
-// later load of that data is the writing wave's own, ordered after its
-// stores (in-order vector memory counter; a single-page unit, whose loads
-// follow at once, waits for the stores).
-__device__ __forceinline__ void append_token(const AttnParams& p, int b, int h, int p0, int npages, int seq, int w,
-                                          int lane) {
-  const int n = (seq + 127) >> 7;
-  if (seq <= 0 || p0 + npages != n) return;
-  const int64_t slot = uniform64(p.new_slot[b]);
-  if (slot < 0) return;
-  const int blk = (int)(slot >> 7);
-  const int64_t kidx = ((int64_t)blk * 2) * p.kvh + h;
-  const uint64_t ka = (uint64_t)uniform64(p.rec_addr[kidx]), va = (uint64_t)uniform64(p.rec_addr[kidx + p.kvh]);
-  const int kl = uniform(p.rec_len[kidx]), vl = uniform(p.rec_len[kidx + p.kvh]);
-  auto writable = [&](uint64_t a, int len) {
-    return len == kRawVarLen && ((a >= p.w_lo0 && a + kRawRecord <= p.w_hi0) || (a >= p.w_lo1 && a + kRawRecord <= p.w_hi1));
-  };
-  const int off = (int)(slot & 127);
-  if (w == (off >> 5) && writable(ka, kl)) {
-    // K: lane = dim pair (2 lane, 2 lane + 1) = 16 st + 8 f + 2 c; token off = 16 tw + 8 j + g
-    const uint32_t val = *reinterpret_cast<const uint32_t*>(p.nk + b * p.nk_s0 + h * p.nk_s1 + 2 * lane);
-    const int st = lane >> 3, f = (lane >> 2) & 1, c = lane & 3;
-    const int tw = off >> 4, j = (off >> 3) & 1, g = off & 7, t = 32 * tw + 4 * g + c;
-    *reinterpret_cast<FP_GLOBAL uint32_t*>(ka + 16 * (256 * st + t) + 2 * (4 * j + 2 * f)) = val;
-  }
-  if (lane < 32 && writable(va, vl)) {
-    // V: dim d = 32 w + lane = 16 tw + 8 j + g; token off = 16 st + 8 f + 2 c + e
-    const int d = 32 * w + lane;
-    const uint16_t val = p.nv[b * p.nv_s0 + h * p.nv_s1 + d];
-    const int st = off >> 4, f = (off >> 3) & 1, c = (off >> 1) & 3, e = off & 1;
-    const int tw = d >> 4, j = (d >> 3) & 1, g = d & 7, t = 32 * tw + 4 * g + c;
-    *reinterpret_cast<FP_GLOBAL uint16_t*>(va + 16 * (256 * st + t) + 2 * (4 * j + 2 * f + e)) = val;
-  }
-  asm volatile("" ::: "memory");
-  if (npages == 1) __builtin_amdgcn_s_waitcnt(0);
-}
-
 // Split-KV merge of (b, h) after this workgroup wrote the partial of one of
 // its ``chunks`` units (``first`` .. ``first + chunks - 1``): the last
 // workgroup to arrive merges all of them with the online-softmax merge in the
@@ -597,7 +546,7 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
       make_uint2(lo, hi);
 }
 
-template <bool kInlinePlan, bool kAppend>
+template <bool kInlinePlan>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kAttnPerCu))) attn_kernel(AttnParams p) {
   __shared__ AttnShared sh;
   const int lane = wave_lane();
@@ -696,7 +645,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       chunks = uniform(u1.y);
       blk0 = uniform(u1.z);
     }
-    if constexpr (kAppend) append_token(p, b, h, p0, npages, seq, w, lane);
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
     // Q rows of the group, issued first so they overlap the record-table
     // hop: wave 0 loads 16-byte pieces L = lane, lane + 64 (row L / 16, u32
@@ -1002,16 +950,10 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   // heads) walks the units in use
   const int64_t per_head = std::min<int64_t>(units, (slots + kv_heads - 1) / kv_heads);
   const dim3 grid((unsigned)per_head, (unsigned)kv_heads), block(64 * kWaves);
-  if (p.nk != nullptr) {
-    if (p.inline_plan)
-      hipLaunchKernelGGL((attn_kernel<true, true>), grid, block, 0, stream, p);
-    else
-      hipLaunchKernelGGL((attn_kernel<false, true>), grid, block, 0, stream, p);
-  } else if (p.inline_plan) {
-    hipLaunchKernelGGL((attn_kernel<true, false>), grid, block, 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((attn_kernel<false, false>), grid, block, 0, stream, p);
-  }
+  if (p.inline_plan)
+    hipLaunchKernelGGL((attn_kernel<true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((attn_kernel<false>), grid, block, 0, stream, p);
   FP_LAUNCH_CHECK();
   return 0;
 }
@@ -1025,7 +967,6 @@ extern "C" int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, i
                                int64_t ml_elems, int32_t* plan, int64_t plan_elems, void* out, int64_t out_stride,
                                int64_t units, int replan, double scale, fp_stream_t stream) {
   AttnParams p{};
-  p.nk = p.nv = nullptr;
   return decode_launch(p, q, q_stride, batch, kv_heads, group, rec_addr, rec_len, plut, slut, block_table, bt_stride,
                        seq_lens, opart, opart_elems, ml, ml_elems, plan, plan_elems, out, out_stride, units, replan,
                        scale, stream);
@@ -1042,30 +983,15 @@ extern "C" int fp_fused_decode_append(const void* q, int64_t q_stride, int64_t b
                                       const int64_t* slot_mapping, const void* staging, int64_t staging_bytes,
                                       const void* scratch, int64_t scratch_bytes, fp_stream_t stream) {
   // Switched off: the first GPU run of its tests faulted the device and the
-  // cause is not found yet (every address the append computes was checked by
-  // reading); the entry stays declared so that callers fail loudly.
-  FP_CHECK(false, "fp_fused_decode_append is disabled: its first GPU run faulted, cause not yet found");
-  FP_CHECK(new_k && new_v && slot_mapping, "append needs the new K and V tokens and their slots");
-  FP_CHECK(reinterpret_cast<uintptr_t>(new_k) % 4 == 0 && nk_token_stride % 2 == 0 && nk_head_stride % 2 == 0,
-           "new K rows must be 4-byte aligned (even strides)");
-  FP_CHECK(nk_token_stride >= 0 && nk_head_stride >= kDim && nv_token_stride >= 0 && nv_head_stride >= kDim,
-           "new K / V must be [B, H, 128] with contiguous head rows");
-  FP_CHECK(staging_bytes >= 0 && scratch_bytes >= 0, "negative record ranges");
-  AttnParams p{};
-  p.nk = static_cast<const uint16_t*>(new_k);
-  p.nv = static_cast<const uint16_t*>(new_v);
-  p.new_slot = slot_mapping;
-  p.nk_s0 = nk_token_stride;
-  p.nk_s1 = nk_head_stride;
-  p.nv_s0 = nv_token_stride;
-  p.nv_s1 = nv_head_stride;
-  p.w_lo0 = reinterpret_cast<uint64_t>(staging);
-  p.w_hi0 = p.w_lo0 + (uint64_t)staging_bytes;
-  p.w_lo1 = reinterpret_cast<uint64_t>(scratch);
-  p.w_hi1 = p.w_lo1 + (uint64_t)scratch_bytes;
-  return decode_launch(p, q, q_stride, batch, kv_heads, group, rec_addr, rec_len, plut, slut, block_table, bt_stride,
-                       seq_lens, opart, opart_elems, ml, ml_elems, plan, plan_elems, out, out_stride, units, replan,
-                       scale, stream);
+  // cause has not been shown; the device code is removed and the entry
+  // stays declared so that callers fail loudly.
+  (void)q, (void)q_stride, (void)batch, (void)kv_heads, (void)group, (void)rec_addr, (void)rec_len, (void)plut;
+  (void)slut, (void)block_table, (void)bt_stride, (void)seq_lens, (void)opart, (void)opart_elems, (void)ml;
+  (void)ml_elems, (void)plan, (void)plan_elems, (void)out, (void)out_stride, (void)units, (void)replan, (void)scale;
+  (void)new_k, (void)nk_token_stride, (void)nk_head_stride, (void)new_v, (void)nv_token_stride, (void)nv_head_stride;
+  (void)slot_mapping, (void)staging, (void)staging_bytes, (void)scratch, (void)scratch_bytes, (void)stream;
+  fp::set_error("fp_fused_decode_append is disabled: its first GPU run faulted and the cause has not been shown");
+  return -1;
 }
 
 // ---------------------------------------------------------------------------
@@ -1133,7 +1059,6 @@ extern "C" int fp_fused_decode_noalloc(const void* q, int64_t q_stride, int64_t 
   uint8_t* base = device_scratch();
   if (base == nullptr) return -1;
   fp::AttnParams p{};
-  p.nk = p.nv = nullptr;
   return fp::decode_launch(p, q, q_stride, batch, kv_heads, group, rec_addr, rec_len, plut, slut, block_table,
                            bt_stride, seq_lens, reinterpret_cast<float*>(base), opart_elems,
                            reinterpret_cast<float*>(base + ml_off), ml_elems,

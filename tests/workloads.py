@@ -56,29 +56,33 @@ def gen_kv(torch, gen, n_tok: int, heads: int, scales_t, heavy: float = 0.0):
 
 
 def build_store(torch, heads: int, n_blocks: int, tables, gen, scales_t, fill_blocks: int, heavy: float = 0.0,
-                overflow: int = 8192, keep_kv: bool = False):
-    """A one-layer store whose blocks 0..n_blocks-1 are written and encoded."""
+                overflow: int = 8192, keep_kv: bool = False, layers: int = 1):
+    """A store of ``layers`` layers whose blocks 0..n_blocks-1 are written and
+    encoded, each layer with KV of its own (same distribution and tables);
+    ``keep_kv`` returns layer 0's KV."""
     from fragpack_amd.compression.attn_tables import device_tables
     from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
 
     dev = torch.device("cuda")
-    arena = torch.empty((n_blocks, page_bytes(heads)), dtype=torch.uint8, device=dev)
-    store = HbmKvStore([arena], heads, device_tables(tables, dev), max_tokens=fill_blocks * T, staging_slots=1,
+    arenas = [torch.empty((n_blocks, page_bytes(heads)), dtype=torch.uint8, device=dev) for _ in range(layers)]
+    tables = np.repeat(np.asarray(tables)[:1], layers, axis=0)
+    store = HbmKvStore(arenas, heads, device_tables(tables, dev), max_tokens=fill_blocks * T, staging_slots=1,
                        overflow_records=overflow)
     kept = []
     no_live = np.zeros(0, np.int32)
     for b0 in range(0, n_blocks, fill_blocks):
         n = min(fill_blocks, n_blocks - b0)
         slots = (torch.arange(b0, b0 + n, device=dev)[:, None] * T + torch.arange(T, device=dev)).reshape(-1)
-        kv = gen_kv(torch, gen, n * T, heads, scales_t, heavy)
         store.prepare(slots, slots.numel(), no_live)
-        store.write(0, kv[0], kv[1], slots)
-        store.encode(0, n)
+        for layer in range(layers):
+            kv = gen_kv(torch, gen, n * T, heads, scales_t, heavy)
+            store.write(layer, kv[0], kv[1], slots)
+            store.encode(layer, n)
+            if keep_kv and layer == 0:
+                kept.append(kv)
         store.commit()
-        if keep_kv:
-            kept.append(kv)
     torch.cuda.synchronize()
-    return store, arena, (torch.cat(kept, dim=1) if keep_kv else None)
+    return store, (arenas[0] if layers == 1 else arenas), (torch.cat(kept, dim=1) if keep_kv else None)
 
 
 def reference_decode(torch, q, kv, block_table, lens, heads, group, scale):
