@@ -69,6 +69,7 @@ struct PagedParams {
   int32_t* done;  // [B, H] merge counters (zero between launches)
   uint16_t* out;
   int64_t q_stride, out_stride, bt_stride;
+  int64_t num_blocks;  // pages in the caches: block ids outside [0, num_blocks) are skipped
   int kvh, group, splits, ppc;
   float scale_log2;
 };
@@ -92,14 +93,19 @@ struct KFrag {
   uint4 k[2][4];  // [16-key tile][k-step]: key 16 t + j, dims 32 ks + 8 q4 .. + 7
 };
 
-__device__ __forceinline__ void load_page(const PagedParams& p, int64_t blk, int h, int w, int valid, int lane,
+// A block id outside the caches reads as an empty page (zero-sized
+// resources: every load returns zero) and the caller masks all its keys;
+// returns whether the page is inside.
+__device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int h, int w, int valid, int lane,
                                           KFrag& kf, uint8_t* vstage) {
   const int j = lane & 15, q4 = lane >> 4;
   const int row = p.kvh * kPgRow;  // bytes between consecutive keys of one head
+  const bool inside = blk >= 0 && blk < p.num_blocks;
+  if (!inside) blk = 0;
   const uint8_t* kpage = reinterpret_cast<const uint8_t*>(p.kc) + (blk * 128 * p.kvh + h) * kPgRow;
   const uint8_t* vpage = reinterpret_cast<const uint8_t*>(p.vc) + (blk * 128 * p.kvh + h) * kPgRow;
-  const rsrc_t rk = make_rsrc(kpage, 128 * row);
-  const rsrc_t rv = make_rsrc(vpage, 128 * row);
+  const rsrc_t rk = make_rsrc(kpage, inside ? 128 * row : 0);
+  const rsrc_t rv = make_rsrc(vpage, inside ? 128 * row : 0);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int key = min(kPgWaveKeys * w + 16 * t + j, valid - 1);
@@ -115,6 +121,7 @@ __device__ __forceinline__ void load_page(const PagedParams& p, int64_t blk, int
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pg_lds_ptr_t)(vstage + 4 * i * kPgRow), 16,
                                              key * row + 16 * ((lane & 15) ^ (r & 15)), 0, 0, 0);
   }
+  return inside;
 }
 
 struct WaveState {
@@ -202,8 +209,10 @@ paged_decode_kernel(PagedParams p) {
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q4 = lane >> 4;
-  const int len = p.seq_lens[b];
-  const int n_pages = (len + 127) >> 7;
+  // pages past the block table's width are not read (a length beyond it is
+  // cut to the table)
+  const int n_pages = min((p.seq_lens[b] + 127) >> 7, (int)p.bt_stride);
+  const int len = min(p.seq_lens[b], 128 * n_pages);
   const int pg0 = c * p.ppc, pg1 = min(n_pages, pg0 + p.ppc);
   const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride;
 
@@ -223,23 +232,23 @@ paged_decode_kernel(PagedParams p) {
   if (pg0 < pg1) {
     KFrag ka, kb;
     auto valid_of = [&](int pg) { return min(128, len - pg * 128); };
-    load_page(p, bt[pg0], h, w, valid_of(pg0), lane, ka, stage0[w]);
+    bool in_a = load_page(p, bt[pg0], h, w, valid_of(pg0), lane, ka, stage0[w]), in_b = false;
     // two pages per trip so that each stage and fragment set is named statically
     for (int pg = pg0; pg < pg1; pg += 2) {
-      if (pg + 1 < pg1) load_page(p, bt[pg + 1], h, w, valid_of(pg + 1), lane, kb, stage1[w]);
+      if (pg + 1 < pg1) in_b = load_page(p, bt[pg + 1], h, w, valid_of(pg + 1), lane, kb, stage1[w]);
       // page pg landed: only the next page's 16 transfers may still be in flight
       if (pg + 1 < pg1)
         __builtin_amdgcn_s_waitcnt(kVmcnt16);
       else
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      page_step(p, qf, ka, stage0[w], pg * 128 + kPgWaveKeys * w, len, lane, st);
+      page_step(p, qf, ka, stage0[w], pg * 128 + kPgWaveKeys * w, in_a ? len : 0, lane, st);
       if (pg + 1 >= pg1) break;
-      if (pg + 2 < pg1) load_page(p, bt[pg + 2], h, w, valid_of(pg + 2), lane, ka, stage0[w]);
+      if (pg + 2 < pg1) in_a = load_page(p, bt[pg + 2], h, w, valid_of(pg + 2), lane, ka, stage0[w]);
       if (pg + 2 < pg1)
         __builtin_amdgcn_s_waitcnt(kVmcnt16);
       else
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      page_step(p, qf, kb, stage1[w], (pg + 1) * 128 + kPgWaveKeys * w, len, lane, st);
+      page_step(p, qf, kb, stage1[w], (pg + 1) * 128 + kPgWaveKeys * w, in_b ? len : 0, lane, st);
     }
   }
   // ---- combine the four waves: thread t -> query head g = t / 32, dims 4 (t % 32) .. ----
@@ -400,6 +409,7 @@ extern "C" int fp_paged_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.q_stride = q_stride;
   p.out_stride = out_stride;
   p.bt_stride = bt_stride;
+  p.num_blocks = num_blocks;
   p.kvh = (int)kv_heads;
   p.group = (int)group;
   p.splits = (int)splits;

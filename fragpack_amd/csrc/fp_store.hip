@@ -1290,168 +1290,253 @@ __global__ void __launch_bounds__(kThreads) encode_records_kernel(const uint16_t
 }
 
 // ---------------------------------------------------------------------------
-// Block blobs (hbm_kv.cu:496-665): a 64-byte header (u32 magic, version, L,
-// H; i64 bytes, digest) and the i32 rec_len table [L, 2, H] in a 4096-padded
-// head, then the records in (layer, kv, head) order.
+// Block blobs: the on-wire form of a closed block (hbm_kv.cu:496-665).  The
+// byte format is kept exactly, since blobs travel between stores and tiers:
+// a 64-byte header (u32 magic "FPKB", version, L, H; i64 declared bytes,
+// table digest; the rest zero), the i32 rec_len table [L, 2, H], padding to
+// a 4096-byte head, then every record in (layer, kv, head) order, each
+// DENSE + var_len bytes (raw: 32 KB).
+//
+// The kernels move one record per wavefront.  A wave finds its record's place
+// in the blob by summing the sizes before it 64 table entries at a time (one
+// DPP reduction per 64), then streams the record through two buffer
+// resources with kCopyDepth 16-byte loads per lane in flight before the first
+// store; the resources' bounds end the record, so lanes past its end neither
+// load nor store and nothing is predicated.
 constexpr uint32_t kBlobMagic = 0x424B5046u;  // "FPKB"
 constexpr uint32_t kBlobVersion = 1;
 constexpr int kBlobFixed = 64;
 constexpr int64_t kBlobAlign = 4096;
 constexpr int kMaxHeads = 16;
 enum : int { kBlobBadHeader = 1, kBlobBadLengths = 2, kBlobNoOverflow = 4 };
+constexpr int kCopyDepth = 8;       // 16-byte loads in flight per lane: 8 KB per wave
+constexpr int kExportWaves = 4;     // records per export workgroup
+constexpr int kImportWaves = 8;     // waves of an import workgroup (one blob layer)
 
 __host__ __device__ __forceinline__ int64_t blob_head_bytes(int L, int H) {
   return (kBlobFixed + 8LL * L * H + kBlobAlign - 1) / kBlobAlign * kBlobAlign;
 }
 
-__device__ long long block_sum(long long v, long long* red) {
+// Copies ``bytes`` (a 16-byte multiple, at most 32 KB) from ``src`` to
+// ``dst`` with the whole wave: each round issues kCopyDepth 16-byte loads per
+// lane (1 KB apart per load), then their stores.  The whole offset is in the
+// lane's offset (with the instruction's immediate), the part the bounds
+// check covers; the wave-uniform offset register stays 0.
+__device__ __forceinline__ void wave_copy_record(uint8_t* dst, const uint8_t* src, int bytes, int lane) {
+  const rsrc_t rs = make_rsrc(src, bytes), rd = make_rsrc(dst, bytes);
+  for (int base = 16 * lane; base < bytes + 16 * lane; base += 1024 * kCopyDepth) {
+    u32x4_t v[kCopyDepth];
 #pragma unroll
-  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o, 64);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  long long t = 0;
+    for (int k = 0; k < kCopyDepth; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, base + 1024 * k, 0, 0);
 #pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) t += red[w];
-  return t;
+    for (int k = 0; k < kCopyDepth; ++k) __builtin_amdgcn_raw_buffer_store_b128(v[k], rd, base + 1024 * k, 0, 0);
+  }
 }
 
-// grid (n, L): workgroup (i, l) copies layer l's records of blocks[i].
-__global__ void __launch_bounds__(kThreads) blob_export_kernel(const int32_t* blocks, const int64_t* rec_addr,
-                                                              const int32_t* rec_len, uint8_t* out, int64_t stride,
-                                                              int64_t* lengths, int L, int H, int NB,
-                                                              int64_t digest) {
-  __shared__ long long red[kThreads / 64];
-  const int i = blockIdx.x, l = blockIdx.y, tid = threadIdx.x, per = 2 * H;
-  const int b = blocks[i];
-  long long before = 0, total = 0;
-  for (int g = tid; g < L * per; g += kThreads) {
-    const long long n = kDenseBytes + rec_len[((int64_t)(g / per) * NB + b) * per + g % per];
-    total += n;
-    if (g / per < l) before += n;
-  }
-  before = block_sum(before, red);
-  total = block_sum(total, red);
+// Sum over entries [0, upto) of ``size(g)`` (each at most 32 KB), 64 entries
+// per step across the wave.
+template <class Size>
+__device__ __forceinline__ int64_t wave_bytes_before(const Size& size, int upto, int lane) {
+  int64_t sum = 0;
+  for (int c = 0; c < upto; c += 64) sum += wave_total<false>(c + lane < upto ? size(c + lane) : 0);
+  return sum;
+}
+
+// grid (ceil(L * 2H / kExportWaves), n): wave w of workgroup x copies record
+// g = x * kExportWaves + w (layer g / 2H, kv-head g % 2H) of blocks[y]; the
+// wave of record 0 also writes the header, the length table and the blob's
+// aligned length.
+__global__ void __launch_bounds__(64 * kExportWaves) blob_export_kernel(const int32_t* blocks, const int64_t* rec_addr,
+                                                                       const int32_t* rec_len, uint8_t* out,
+                                                                       int64_t stride, int64_t* lengths, int L, int H,
+                                                                       int NB, int64_t digest) {
+  const int lane = wave_lane(), w = uniform((int)(threadIdx.x >> 6));
+  const int i = blockIdx.y, per = 2 * H, count = L * per;
+  const int g = (int)blockIdx.x * kExportWaves + w;
+  const int b = uniform(blocks[i]);
+  // table entry of record gg: rec_len[layer][b][kv-head]
+  auto entry = [&](int gg) { return ((int64_t)(gg / per) * NB + b) * per + gg % per; };
+  auto size = [&](int gg) { return kDenseBytes + rec_len[entry(gg)]; };
+  uint8_t* blob = out + (int64_t)i * stride;
   const int64_t head = blob_head_bytes(L, H);
-  uint8_t* dst = out + (int64_t)i * stride;
-  if (l == 0) {
-    if (tid == 0) {
-      uint32_t* h32 = reinterpret_cast<uint32_t*>(dst);
-      h32[0] = kBlobMagic;
-      h32[1] = kBlobVersion;
-      h32[2] = L;
-      h32[3] = H;
-      int64_t* h64 = reinterpret_cast<int64_t*>(dst + 16);
-      h64[0] = head + total;
-      h64[1] = digest;
-      lengths[i] = (head + total + kBlobAlign - 1) / kBlobAlign * kBlobAlign;
+  if (g == 0) {
+    int64_t total = 0;
+    int32_t* table = reinterpret_cast<int32_t*>(blob + kBlobFixed);
+    for (int c = 0; c < count; c += 64) {
+      int n = 0;
+      if (c + lane < count) {
+        const int len = rec_len[entry(c + lane)];
+        table[c + lane] = len;
+        n = kDenseBytes + len;
+      }
+      total += wave_total<false>(n);
     }
-    int32_t* table = reinterpret_cast<int32_t*>(dst + kBlobFixed);
-    for (int g = tid; g < L * per; g += kThreads) table[g] = rec_len[((int64_t)(g / per) * NB + b) * per + g % per];
+    if (lane < kBlobFixed / 8) {
+      // header words as eight u64 lanes: (magic, version), (L, H), bytes, digest, zeros
+      const uint64_t word[4] = {(uint64_t)kBlobVersion << 32 | kBlobMagic, (uint64_t)(uint32_t)H << 32 | (uint32_t)L,
+                                (uint64_t)(head + total), (uint64_t)digest};
+      reinterpret_cast<uint64_t*>(blob)[lane] = lane < 4 ? word[lane] : 0;
+    }
+    if (lane == 0) lengths[i] = (head + total + kBlobAlign - 1) / kBlobAlign * kBlobAlign;
   }
-  int64_t off = head + before;
-  for (int kvh = 0; kvh < per; ++kvh) {
-    const int64_t idx = ((int64_t)l * NB + b) * per + kvh;
-    const int n = kDenseBytes + rec_len[idx];
-    const uint8_t* srcp = reinterpret_cast<const uint8_t*>(rec_addr[idx]);
-    for (int q = tid; q < n / 16; q += kThreads)
-      *reinterpret_cast<uint4*>(dst + off + 16 * q) = ld16(srcp + 16 * q);
-    off += n;
-  }
+  if (g >= count) return;
+  const int64_t at = head + wave_bytes_before(size, g, lane);
+  const int64_t e = entry(g);
+  const int n = uniform(kDenseBytes + rec_len[e]);
+  wave_copy_record(blob + at, reinterpret_cast<const uint8_t*>(uniform64(rec_addr[e])), n, lane);
 }
 
-// grid (n, L): validates blob i and installs its layer-l records into
-// blocks[i]: coded records packed into the block's arena page, raw ones
-// (and coded ones that no longer fit) in overflow slots.  A failing blob
-// sets status[i] and leaves the layer's tables untouched.
-__global__ void __launch_bounds__(kThreads) blob_import_kernel(Store s, const uint8_t* src, int64_t src_bytes,
-                                                              const int64_t* offsets, const int32_t* blocks,
-                                                              int32_t* status, const int64_t* arena_base,
-                                                              const int64_t* arena_stride, int64_t digest) {
-  __shared__ long long red[kThreads / 64];
-  __shared__ int64_t s_src[2 * kMaxHeads], s_dst[2 * kMaxHeads];
-  __shared__ int s_fail;
-  const int i = blockIdx.x, l = blockIdx.y, tid = threadIdx.x, L = s.L, per = 2 * s.H;
-  const int b = blocks[i];
-  const int64_t off = offsets[i], head = blob_head_bytes(L, s.H);
-  if (off < 0 || off % 16 || off + head > src_bytes) {
-    if (tid == 0) atomicOr(&status[i], kBlobBadHeader);
+// Claims one overflow slot for every lane with ``want`` set (a wave claims
+// for up to 64 records at once).  Lanes read 64 consecutive bitmap words from
+// word ``hint`` on; the wave ranks their free bits, each lane takes with one
+// atomicOr the free bits that serve the next unserved claims, and the bits
+// won are handed to the claiming lanes in rank order.  Bits another caller
+// took meanwhile are retried while the window still shows free bits, then
+// the next 64 words are read.  Returns the lane's slot, or -1 if the pool
+// ran out (slots won for other lanes are kept: the caller frees them).
+__device__ int ovf_alloc_many(const Store& s, uint32_t hint, bool want, int lane) {
+  const uint64_t wanting = __ballot(want);
+  const int need = __popcll(wanting);
+  const int rank = __popcll(wanting & ((1ull << lane) - 1));
+  const uint32_t nw = (uint32_t)s.ovf_words;
+  int got = 0, slot = -1;
+  for (uint32_t base = 0; base < nw && got < need; base += 64) {
+    const uint32_t wi = base + (uint32_t)lane;
+    const int word = wi < nw ? (int)((hint + wi) % nw) : 0;
+    uint32_t cur = wi < nw ? __hip_atomic_load(&s.ovf_bits[word], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0xffffffffu;
+    while (got < need && __ballot(cur != 0xffffffffu)) {
+      const int free_n = __popc(~cur);
+      const int before = wave_incl_scan(free_n) - free_n;
+      const int take = max(0, min(free_n, need - got - before));
+      uint32_t mask = 0, avail = ~cur;
+      for (int k = 0; k < take; ++k) {
+        mask |= avail & (0u - avail);  // lowest free bit
+        avail &= avail - 1;
+      }
+      const uint32_t prev = mask ? atomicOr(&s.ovf_bits[word], mask) : cur;
+      const uint32_t won = mask & ~prev;
+      cur = prev | mask;
+      // hand the won bits to the claiming lanes in rank order
+      for (uint64_t owners = __ballot(won != 0); owners; owners &= owners - 1) {
+        const int j = __builtin_ctzll(owners);
+        uint32_t bits = __builtin_amdgcn_readlane(won, j);
+        const int wj = __builtin_amdgcn_readlane(word, j);
+        for (; bits; bits &= bits - 1, ++got)
+          if (want && rank == got) slot = 32 * wj + __builtin_ctz(bits);
+      }
+    }
+  }
+  return slot;
+}
+
+// Checks blob i's header and whole length table; every wave of every layer's
+// workgroup runs it on its own (scalar loads and one pass over the table),
+// so no workgroup waits for another.  Returns the failure bit (0: valid) and
+// the bytes of the layers before ``l``.
+__device__ int blob_check(const uint8_t* src, int64_t src_bytes, int64_t off, int L, int H, int l, int64_t digest,
+                          int lane, int64_t& before_layer) {
+  const int per = 2 * H, count = L * per;
+  const int64_t head = blob_head_bytes(L, H);
+  if (off < 0 || off % 16 || off + head > src_bytes) return kBlobBadHeader;
+  const uint8_t* blob = src + off;
+  const uint32_t magic = uniform(ld4(blob)), version = uniform(ld4(blob + 4));
+  const int bl = uniform((int)ld4(blob + 8)), bh = uniform((int)ld4(blob + 12));
+  const uint2 d0 = ld8(blob + 16), d1 = ld8(blob + 24);
+  const int64_t declared = (int64_t)((uint64_t)uniform(d0.y) << 32 | uniform(d0.x));
+  const int64_t dig = (int64_t)((uint64_t)uniform(d1.y) << 32 | uniform(d1.x));
+  if (magic != kBlobMagic || version != kBlobVersion || bl != L || bh != H || dig != digest || declared < head ||
+      off + declared > src_bytes)
+    return kBlobBadHeader;
+  const int32_t* table = reinterpret_cast<const int32_t*>(blob + kBlobFixed);
+  int64_t total = 0;
+  before_layer = 0;
+  bool bad = false;
+  for (int c = 0; c < count; c += 64) {
+    int n = 0, nb = 0;
+    if (c + lane < count) {
+      const int v = table[c + lane];
+      if (v == kRawVarLen || (v >= kHeaderBytes && v <= kVarCap && v % 16 == 0))
+        n = kDenseBytes + v;
+      else
+        bad = true;
+      nb = (c + lane) / per < l ? n : 0;
+    }
+    total += wave_total<false>(n);
+    before_layer += wave_total<false>(nb);
+  }
+  if (__ballot(bad) || head + total != declared) return kBlobBadLengths;
+  return 0;
+}
+
+// grid (n, L), kImportWaves waves: workgroup (i, l) validates blob i and
+// installs its layer-l records into blocks[i].  In (kv, head) order a coded
+// record goes to the block's arena page at the page's running fill if it
+// fits, otherwise -- and every raw record -- to an overflow slot; wave 0
+// decides the placement (lanes = records), claims all its overflow slots at
+// once, and on a full pool returns them and fails the layer, whose tables
+// stay untouched.  Every wave then copies its records (one per wave at a
+// time) and wave 0 installs the tables, freeing overflow slots the block's
+// old records held.
+__global__ void __launch_bounds__(64 * kImportWaves) blob_import_kernel(Store s, const uint8_t* src, int64_t src_bytes,
+                                                                       const int64_t* offsets, const int32_t* blocks,
+                                                                       int32_t* status, const int64_t* arena_base,
+                                                                       const int64_t* arena_stride, int64_t digest) {
+  __shared__ int64_t s_from[2 * kMaxHeads], s_to[2 * kMaxHeads];
+  __shared__ int s_ok;
+  const int lane = wave_lane(), w = uniform((int)(threadIdx.x >> 6));
+  const int i = blockIdx.x, l = blockIdx.y, L = s.L, H = s.H, per = 2 * H;
+  const int b = uniform(blocks[i]);
+  const int64_t off = uniform64(offsets[i]);
+  int64_t before_layer = 0;
+  const int fail = blob_check(src, src_bytes, off, L, H, l, digest, lane, before_layer);
+  if (fail) {
+    if (threadIdx.x == 0) atomicOr(&status[i], fail);
     return;
   }
   const uint8_t* blob = src + off;
-  const uint32_t* h32 = reinterpret_cast<const uint32_t*>(blob);
-  const int64_t* h64 = reinterpret_cast<const int64_t*>(blob + 16);
-  const int64_t declared = h64[0];
-  if (h32[0] != kBlobMagic || h32[1] != kBlobVersion || (int)h32[2] != L || (int)h32[3] != s.H ||
-      h64[1] != digest || declared < head || off + declared > src_bytes) {
-    if (tid == 0) atomicOr(&status[i], kBlobBadHeader);
-    return;
-  }
-  const int32_t* table = reinterpret_cast<const int32_t*>(blob + kBlobFixed);
-  long long before = 0, total = 0;
-  int bad = 0;
-  for (int g = tid; g < L * per; g += kThreads) {
-    const int v = table[g];
-    const bool ok = v == kRawVarLen || (v >= kHeaderBytes && v <= kVarCap && v % 16 == 0);
-    bad |= !ok;
-    const long long n = kDenseBytes + (ok ? v : 0);
-    total += n;
-    if (g / per < l) before += n;
-  }
-  bad = __syncthreads_or(bad);
-  before = block_sum(before, red);
-  total = block_sum(total, red);
-  if (bad || head + total != declared) {
-    if (tid == 0) atomicOr(&status[i], kBlobBadLengths);
-    return;
-  }
-  const int32_t* lens = table + l * per;
-  if (tid < 64) {  // wave 0: every lane runs the same placement, the allocator uses the wave
-    const int64_t page = arena_stride[l];
-    const int64_t page_ptr = arena_base[l] + (int64_t)b * page;
-    int64_t from = head + before;
-    int fill = 0, placed = 0;
-    for (; placed < per; ++placed) {
-      const int n = kDenseBytes + lens[placed];
-      int64_t d;
-      if (lens[placed] != kRawVarLen && fill + n <= page) {
-        d = page_ptr + fill;
-        fill += n;
-      } else {
-        const int slot = ovf_alloc_wave(s, (uint32_t)(b * per + placed), tid);
-        if (slot < 0) break;
-        d = reinterpret_cast<int64_t>(s.ovf_base) + (int64_t)slot * kRawRecord;
+  const int32_t* lens = reinterpret_cast<const int32_t*>(blob + kBlobFixed) + l * per;
+  if (w == 0) {
+    const int len = lane < per ? lens[lane] : 0;
+    const int n = kDenseBytes + len;
+    // page placement in (kv, head) order: a coded record takes the page's
+    // running fill when it fits (the rule is sequential: a record that does
+    // not fit leaves the fill for the smaller ones after it)
+    const int64_t page = uniform64(arena_stride[l]);
+    int fill = 0, at = -1;
+    for (int k = 0; k < per; ++k) {
+      const int nk = __builtin_amdgcn_readlane(n, k);
+      if (__builtin_amdgcn_readlane(len, k) != kRawVarLen && fill + nk <= page) {
+        if (lane == k) at = fill;
+        fill += nk;
       }
-      if (tid == 0) {
-        s_src[placed] = from;
-        s_dst[placed] = d;
-      }
-      from += n;
     }
-    if (tid == 0) {
-      s_fail = placed < per;
-      if (s_fail) {
-        for (int k = 0; k < placed; ++k) ovf_free(s, s_dst[k]);
-        atomicOr(&status[i], kBlobNoOverflow);
-      } else {
-        s.fill[(int64_t)l * s.NB + b] = fill;
-      }
+    const int from = wave_incl_scan(lane < per ? n : 0) - n;  // the record's bytes past the layer's first
+    const bool ovf = lane < per && at < 0;
+    const int slot = ovf_alloc_many(s, (uint32_t)(b * per), ovf, lane);
+    const bool ok = !__ballot(ovf && slot < 0);
+    if (!ok) {
+      if (ovf && slot >= 0) ovf_free(s, reinterpret_cast<int64_t>(s.ovf_base) + (int64_t)slot * kRawRecord);
+      if (lane == 0) atomicOr(&status[i], kBlobNoOverflow);
+    } else if (lane < per) {
+      s_from[lane] = blob_head_bytes(L, H) + before_layer + from;
+      s_to[lane] = ovf ? reinterpret_cast<int64_t>(s.ovf_base) + (int64_t)slot * kRawRecord
+                       : uniform64(arena_base[l]) + (int64_t)b * page + at;
+    }
+    if (lane == 0) {
+      s_ok = ok;
+      if (ok) s.fill[(int64_t)l * s.NB + b] = fill;
     }
   }
   __syncthreads();
-  if (s_fail) return;
-  for (int kvh = 0; kvh < per; ++kvh) {
-    const uint8_t* from = blob + s_src[kvh];
-    uint8_t* to = reinterpret_cast<uint8_t*>(s_dst[kvh]);
-    for (int q = tid; q < (kDenseBytes + lens[kvh]) / 16; q += kThreads)
-      *reinterpret_cast<uint4*>(to + 16 * q) = *reinterpret_cast<const uint4*>(from + 16 * q);
-  }
-  __syncthreads();
-  if (tid < per) {
-    const int64_t idx = ((int64_t)l * s.NB + b) * per + tid;
-    ovf_free(s, s.rec_addr[idx]);
-    s.rec_addr[idx] = s_dst[tid];
-    s.rec_len[idx] = lens[tid];
+  if (!s_ok) return;
+  for (int k = w; k < per; k += kImportWaves)
+    wave_copy_record(reinterpret_cast<uint8_t*>(s_to[k]), blob + s_from[k], uniform(kDenseBytes + lens[k]), lane);
+  if (w == 0 && lane < per) {
+    const int64_t e = ((int64_t)l * s.NB + b) * per + lane;
+    ovf_free(s, s.rec_addr[e]);
+    s.rec_addr[e] = s_to[lane];
+    s.rec_len[e] = lens[lane];
   }
 }
 
@@ -1647,7 +1732,10 @@ extern "C" int fp_hbm_export(const int32_t* blocks, int64_t n, const int64_t* re
                stride >= blob_head_bytes((int)num_layers, (int)kv_heads) + 2LL * num_layers * kv_heads * kRawRecord &&
                out_bytes >= n * stride,
            "export stride or buffer too small");
-  hipLaunchKernelGGL(blob_export_kernel, dim3((unsigned)n, (unsigned)num_layers), dim3(kThreads), 0, stream, blocks,
+  const int64_t count = 2 * num_layers * kv_heads;
+  FP_CHECK(n < 65536 && count < (1LL << 24), "too many blobs or records per blob in one export");
+  hipLaunchKernelGGL(blob_export_kernel, dim3((unsigned)((count + kExportWaves - 1) / kExportWaves), (unsigned)n),
+                     dim3(64 * kExportWaves), 0, stream, blocks,
                      rec_addr, rec_len, out, stride, lengths, (int)num_layers, (int)kv_heads, (int)num_blocks, digest);
   FP_LAUNCH_CHECK();
   return 0;
@@ -1661,7 +1749,8 @@ extern "C" int fp_hbm_import(const fp_store_t* d, const uint8_t* src, int64_t sr
   FP_CHECK(d->kv_heads <= kMaxHeads, "too many KV heads");
   FP_CHECK(reinterpret_cast<uintptr_t>(src) % 16 == 0, "import buffer must be contiguous 16-byte aligned uint8");
   const Store s = make_store(d);
-  hipLaunchKernelGGL(blob_import_kernel, dim3((unsigned)n, (unsigned)d->num_layers), dim3(kThreads), 0, stream, s,
+  FP_CHECK(d->num_layers < 65536, "too many layers for one import launch");
+  hipLaunchKernelGGL(blob_import_kernel, dim3((unsigned)n, (unsigned)d->num_layers), dim3(64 * kImportWaves), 0, stream, s,
                      src, src_bytes, offsets, blocks, status, arena_base, arena_stride, digest);
   FP_LAUNCH_CHECK();
   return 0;

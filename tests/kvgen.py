@@ -71,12 +71,18 @@ def make_tables(rng: np.random.Generator, heads: int, outlier: float, scales: np
 
 
 def decode_case(seed: int, batch: int, heads: int, group: int, lens, outlier: float = 0.02,
-                raw_tail: bool = True, extra_blocks: int = 2) -> DecodeCase:
+                raw_tail: bool = True, extra_blocks: int = 2, poke=None, scales=None, tables=None) -> DecodeCase:
+    """A seeded decode case; ``poke(kv, block_table)`` may edit the token-major
+    KV bits [NB, 2, T, H, D] before the records are built.  ``scales``
+    ([2, H, 128]) and ``tables`` ([2, H, 22]) replace the drawn channel scales
+    and the calibrated tables."""
     rng = np.random.default_rng(seed)
     lens = np.asarray(lens, np.int32)
     assert lens.size == batch
-    scales = np.stack([[channel_scale(rng, D, outlier) for _ in range(heads)] for _ in range(2)])
-    tables = make_tables(rng, heads, outlier, scales)
+    if scales is None:
+        scales = np.stack([[channel_scale(rng, D, outlier) for _ in range(heads)] for _ in range(2)])
+    if tables is None:
+        tables = make_tables(rng, heads, outlier, scales)
     pages = [(int(n) + T - 1) // T for n in lens]
     nb = sum(pages) + extra_blocks
     perm = rng.permutation(nb).astype(np.int32)
@@ -93,6 +99,8 @@ def decode_case(seed: int, batch: int, heads: int, group: int, lens, outlier: fl
     for k in range(2):
         for h in range(heads):
             kv[:, k, :, h, :] = kv_bits(rng, (nb, T, D), outlier, scales[k, h])
+    if poke is not None:
+        poke(kv, bt)
     # records, 16-byte aligned, in one arena
     chunks = []
     rec_off = np.zeros((nb, 2, heads), np.int64)
@@ -131,11 +139,13 @@ def reference_attention(case: DecodeCase) -> np.ndarray:
             k = bits_to_f32(case.kv[blks, 0, :, h, :]).reshape(-1, D)[:n].astype(np.float64)
             v = bits_to_f32(case.kv[blks, 1, :, h, :]).reshape(-1, D)[:n].astype(np.float64)
             qh = q[b, h * G : (h + 1) * G]
-            s = qh @ k.T * case.scale
-            s -= s.max(axis=1, keepdims=True)
-            p = np.exp(s)
-            p /= p.sum(axis=1, keepdims=True)
-            out[b, h * G : (h + 1) * G] = (p @ v).astype(np.float32)
+            with np.errstate(invalid="ignore", over="ignore"):
+                # NaN / Inf bits propagate as IEEE arithmetic does
+                s = qh @ k.T * case.scale
+                s -= s.max(axis=1, keepdims=True)
+                p = np.exp(s)
+                p /= p.sum(axis=1, keepdims=True)
+                out[b, h * G : (h + 1) * G] = (p @ v).astype(np.float32)
     return out
 
 
@@ -181,3 +191,31 @@ def run_gpu_decode(case: DecodeCase, units: int | None = None, repeat: int = 1) 
     torch.cuda.synchronize()
     del arena
     return out.float().cpu().numpy()
+
+
+def config0_case(workdir, seed: int = 0) -> DecodeCase:
+    """1 sequence, 4 KV heads, GQA 8, 1000 tokens (7 coded
+    blocks + a 104-token raw tail), 2% outlier channels; the tables come from
+    the repository's calibration CLI (``python -m
+    fragpack_amd.compression.attn_tables dump.npy tables.npz``) run on a seeded
+    uint16 dump [64, 1, 2, 128, 4, 128] drawn from the same distribution."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    H = 4
+    rng = np.random.default_rng(seed)
+    scales = np.stack([[channel_scale(rng, D, 0.02) for _ in range(H)] for _ in range(2)])
+    dump = np.empty((64, 1, 2, T, H, D), np.uint16)
+    for kv in range(2):
+        for h in range(H):
+            dump[:, 0, kv, :, h, :] = kv_bits(rng, (64, T, D), 0.02, scales[kv, h])
+    workdir = Path(workdir)
+    np.save(workdir / "dump.npy", dump)
+    root = Path(__file__).resolve().parent.parent
+    subprocess.run([sys.executable, "-m", "fragpack_amd.compression.attn_tables", str(workdir / "dump.npy"),
+                    str(workdir / "tables.npz")], check=True, cwd=root, capture_output=True)
+    with np.load(workdir / "tables.npz", allow_pickle=False) as f:
+        tables = f["table"]
+    assert tables.shape == (1, 2, H, 22)
+    return decode_case(seed + 1, batch=1, heads=H, group=8, lens=[1000], scales=scales, tables=tables[0])

@@ -28,10 +28,27 @@ def _check(out, ref, lens=None):
         assert not np.any(out[np.asarray(lens) == 0])
 
 
-def test_config0_shape():
-    """1 seq, H4, G8, 1000 tokens: 7 coded pages + a 104-token raw tail."""
-    case = kvgen.decode_case(seed=0, batch=1, heads=4, group=8, lens=[1000], outlier=0.02)
+def test_config0_shape(tmp_path):
+    """1 seq, H4, G8, 1000 tokens (7 coded pages + a
+    104-token raw tail), tables from the repository's calibration CLI on a
+    seeded [64, 1, 2, 128, 4, 128] dump.  The GPU batch codec reconstructs
+    every record bit-exactly, and decode attention matches float64."""
+    from fragpack_amd.compression import attn_page as ap
+
+    case = kvgen.config0_case(tmp_path)
     print("config0 case built", flush=True)
+    blks = case.block_table[0, :8]
+    recs, kvs, tabs, want = [], [], [], []
+    for blk in blks:
+        for kv in range(2):
+            for h in range(4):
+                off = int(case.rec_off[blk, kv, h])
+                recs.append(case.recs[off : off + kvgen.DENSE + int(case.rec_len[blk, kv, h])].tobytes())
+                kvs.append(kv)
+                tabs.append(kv * 4 + h)
+                want.append(case.kv[blk, kv, :, h, :])
+    back = ap.decode_records(recs, case.tables.reshape(8, 22), np.array(kvs, np.int32), np.array(tabs, np.int32))
+    np.testing.assert_array_equal(back, np.stack(want))
     out = kvgen.run_gpu_decode(case)
     _check(out, kvgen.reference_attention(case))
 

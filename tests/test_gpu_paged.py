@@ -89,3 +89,38 @@ def test_paged_decode_long_context_config1_shape():
     paged_decode_attention(q, kc, vc, bt, lt, 8192, D ** -0.5, out, ws, splits)
     torch.cuda.synchronize()
     torch.testing.assert_close(out.float(), _reference(q, kc, vc, bt, lt, 4, 8), atol=2e-2, rtol=1e-2)
+
+
+def test_paged_decode_skips_pages_outside_the_cache():
+    """Device data the host cannot see: a block id outside [0, num_blocks)
+    (here -1 and num_blocks + 5) is skipped like a masked page, and a length
+    beyond the block table's width is cut to the table -- nothing outside
+    the caches or the table row is read."""
+    import torch
+
+    from fragpack_amd.ops.paged_attn import paged_decode_attention, paged_workspace
+
+    heads, group = 2, 4
+    lens = [512, 512, 512]
+    q, kc, vc, bt, lt = _case(77, lens, heads, group)
+    nb = kc.shape[0]
+    bt_bad = bt.clone()
+    bt_bad[0, 1] = -1
+    bt_bad[1, 3] = nb + 5
+    lt_long = lt.clone()
+    lt_long[2] = 4000  # the table has 4 pages: 512 keys are read
+    # references: sequence 0 without page 1, sequence 1 without page 3
+    keep = [[0, 2, 3], [0, 1, 2], [0, 1, 2, 3]]
+    ref = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+    for b in range(3):
+        k = kc[bt[b, keep[b]].long()].reshape(-1, heads, D).float()
+        v = vc[bt[b, keep[b]].long()].reshape(-1, heads, D).float()
+        s = torch.einsum("hgd,thd->hgt", q[b].float().view(heads, group, D), k) * D ** -0.5
+        ref[b] = torch.einsum("hgt,thd->hgd", s.softmax(-1), v).reshape(heads * group, D)
+    for splits in (1, 2, 4):
+        print("paged bounds case", splits, flush=True)
+        ws = paged_workspace(3, heads, splits, q.device)
+        out = torch.full_like(q, float("nan"))
+        paged_decode_attention(q, kc, vc, bt_bad, lt_long, 512, D ** -0.5, out, ws, splits)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.float(), ref, atol=2e-2, rtol=1e-2)

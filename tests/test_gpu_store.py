@@ -461,6 +461,32 @@ def test_blob_import_rejects_bad_blobs_untouched():
     assert torch.equal(dst.store.rec_addr[0, 10], before[0][0, 10])
 
 
+def test_blob_import_partial_overflow_claim_is_returned():
+    """A layer needing two overflow slots finds one: the slot it won goes back
+    to the pool and that layer's tables stay as they were, while the blob's
+    other layer (coded records only) installs; the export's header words past
+    the digest are zero."""
+    import torch
+
+    src = SimEngine(0, noisy={(3, 0, 0, 1), (3, 0, 1, 0)})
+    _serve(src)
+    blobs, _ = _export(src, [3])
+    assert not blobs[32:64].any()
+    dst = SimEngine(0, overflow=1)
+    before = dst.store.rec_addr.clone(), dst.store.rec_len.clone()
+    assert _import(dst, blobs, [0], [8]) == [4]
+    torch.cuda.synchronize()
+    assert _overflow_in_use(dst) == 0
+    assert torch.equal(dst.store.rec_addr[0, 8], before[0][0, 8]) and torch.equal(dst.store.rec_len[0, 8], before[1][0, 8])
+    assert torch.equal(dst.store.rec_len[1, 8], src.store.rec_len[1, 3])
+    ids = torch.tensor([8], dtype=torch.int32, device="cuda")
+    wk = torch.empty(1, T, dst.H, D, dtype=torch.bfloat16, device="cuda")
+    wv = torch.empty_like(wk)
+    dst.store.gather(1, ids, wk, wv)
+    for k, x in enumerate((wk, wv)):
+        np.testing.assert_array_equal(x.view(torch.int16).cpu().numpy().view(np.uint16)[0], src.kv[1, k, 3])
+
+
 def test_fused_write_encode_degenerate_steps():
     """write_encode with nothing to close (the write alone), with no tokens
     (the encode alone) and with padding slots (-1) leaves the same records
