@@ -50,6 +50,13 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 4;     // wavefronts per workgroup = slabs per record
 constexpr int kBtLds = 1024;  // block-table entries a planning launch may hold in LDS
 constexpr int kAttnPerCu = 3;  // resident workgroups per CU (kWaves = SIMDs per CU; VGPR budget 512 / 3)
+// Launches with few (sequence, KV head) pairs split every sequence into many
+// chunks, and the merge of a pair's partials (one workgroup reading 4 KB per
+// chunk through one CU) sets their tail.  They run workgroups of two halves
+// (8 waves, one workgroup per CU): each half is a 4-wave unit walking every
+// other page of the workgroup's chunk, the halves combine in LDS, and a pair
+// has half the chunks to merge.
+constexpr int kHalvesPairs = 32;  // batch x kv_heads up to which launches use two halves
 constexpr float kLazyMax = 8.f;    // log2 headroom of the speculative softmax reference
 constexpr int kTileRow = 4 * 4 * 16 + 16;   // one head's row of a fragment tile, padded by a chunk
 constexpr int kTileBytes = 8 * kTileRow;    // Q / P fragment tile: [head 8][a 4][c 4] x 16 B
@@ -73,6 +80,7 @@ struct AttnParams {
   int kvh, group, units, batch;
   int ud_off;  // int32 offset of the unit descriptors in plan
   int slots;   // resident workgroups of this kernel on the device
+  int halves;  // 2: two 4-wave halves per workgroup, each taking every other page
   int inline_plan;  // 1: every workgroup plans for itself (batch <= 64)
   int bt_lds;       // inline plan and the whole block table (batch x bt_stride <= kBtLds) read into LDS
   float scale_log2;
@@ -128,7 +136,7 @@ struct Divider {  // x / d for 0 <= x < 2^24, 1 <= d
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __restrict__ seq_lens,
                                                             const int32_t* __restrict__ block_table, int64_t bt_stride,
                                                             int32_t* __restrict__ plan, int64_t plan_elems, int batch,
-                                                            int units, int kvh, int slots) {
+                                                            int units, int kvh, int slots, int halves) {
   __shared__ int firsts[kPlanLds + 1];
   __shared__ unsigned long long best;
   __shared__ int shared_used;
@@ -164,7 +172,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const int32_t* __res
     const int n = count_chunks(ppc);
     if (n <= units && lane == 0) {
       const int64_t rounds = ((int64_t)n * kvh + slots - 1) / slots;
-      const uint64_t cost = (uint64_t)(rounds * (ppc + kUnitCost));
+      const uint64_t cost = (uint64_t)(rounds * ((ppc + halves - 1) / halves + kUnitCost));
       atomicMin(&best, (cost << 24) | (uint64_t)(0xFFFFFF - ppc));
     }
   }
@@ -409,12 +417,13 @@ __device__ __forceinline__ void decode_slab(const RecRef& r, const SlabBuf& b, i
   decode_words<true>(b, esc, e0 + excl, lut.p0, lut.p1, emit);
 }
 
-struct AttnShared {
+struct alignas(16) AttnShared {
   uint8_t esc[2][2][kEscLds];  // [page parity][K, V] expanded escape bytes
   uint32_t hdr[2][2][12];      // [page parity][K, V] record headers
   uint8_t pt[kTileBytes];      // P tile
   uint8_t qt[kTileBytes];      // Q tile, even-odd slot order
   float red[kWaves][8];        // per-wave page max / final l per head
+  float mrun[8];               // the running max per head before this page (two-half workgroups)
   int last;
 };
 
@@ -466,7 +475,7 @@ __device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane)
   uint64_t key = ~0ull;
   if (chunks <= p.units) {
     const int64_t rounds = ((int64_t)chunks * p.kvh + p.slots - 1) / p.slots;
-    key = ((uint64_t)(rounds * (cand + kUnitCost)) << 24) | (uint64_t)(0xFFFFFF - cand);
+    key = ((uint64_t)(rounds * ((cand + p.halves - 1) / p.halves + kUnitCost)) << 24) | (uint64_t)(0xFFFFFF - cand);
   }
   key = wave_min_u64(key);
   r.ppc = uniform(0xFFFFFF - (int)(key & 0xFFFFFFu));
@@ -546,11 +555,15 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
       make_uint2(lo, hi);
 }
 
-template <bool kInlinePlan>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kAttnPerCu))) attn_kernel(AttnParams p) {
-  __shared__ AttnShared sh;
+template <bool kInlinePlan, int kHalves>
+__global__ void __launch_bounds__(64 * kWaves * kHalves) __attribute__((amdgpu_waves_per_eu(kAttnPerCu)))
+attn_kernel(AttnParams p) {
+  __shared__ AttnShared shs[kHalves];
   const int lane = wave_lane();
-  const int w = uniform((int)(threadIdx.x >> 6));  // this wave's slab of every record (wave-uniform)
+  const int wave = uniform((int)(threadIdx.x >> 6));
+  const int w = wave & (kWaves - 1);          // this wave's slab of every record (wave-uniform)
+  const int half = kHalves == 2 ? wave >> 2 : 0;  // this wave's half of the workgroup
+  AttnShared& sh = shs[half];
   const int h = blockIdx.y;
   const int c = lane >> 4, hh = (lane >> 3) & 1, g = lane & 7;
   const int nt = 32 * hh + 4 * g + c;
@@ -566,11 +579,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // global round trip after the plan is known.
   __shared__ int bt_s[kInlinePlan ? kBtLds : 1];
   // the inline plan per wave: first unit, chunks, context, pages by sequence
-  __shared__ int plan_s[kInlinePlan ? kWaves : 1][4][64];
-  int(&wplan)[4][64] = plan_s[kInlinePlan ? w : 0];  // this wave's rows
+  __shared__ int plan_s[kInlinePlan ? kWaves * kHalves : 1][4][64];
+  int(&wplan)[4][64] = plan_s[kInlinePlan ? wave : 0];  // this wave's rows
   const bool bt_lds = kInlinePlan && p.bt_lds;
   if (bt_lds)
-    for (int i = threadIdx.x; i < p.batch * (int)p.bt_stride; i += 64 * kWaves) bt_s[i] = p.block_table[i];
+    for (int i = threadIdx.x; i < p.batch * (int)p.bt_stride; i += 64 * kWaves * kHalves) bt_s[i] = p.block_table[i];
   if constexpr (kInlinePlan) ip = inline_plan(p, lane);
   if (bt_lds) __syncthreads();
   const int used = kInlinePlan ? ip.used : uniform(p.plan[1]);  // units in use
@@ -586,7 +599,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // reads for the compiler too (the wave's LDS accesses are in order)
     wave_lds_sync();
   }
-  if (kInlinePlan && blockIdx.x == 0 && h == 0 && w == 0) {
+  if (kInlinePlan && blockIdx.x == 0 && h == 0 && wave == 0) {
     // the plan words for later calls that reuse this plan
     int32_t* plan = p.plan;
     if (lane < p.batch) {
@@ -601,14 +614,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   if (kInlinePlan && h == 0) {
     // idle units of this workgroup's stride
     int32_t* plan = p.plan;
-    for (int u = blockIdx.x + gridDim.x * (int)threadIdx.x; u < p.units; u += gridDim.x * 64 * kWaves)
+    for (int u = blockIdx.x + gridDim.x * (int)threadIdx.x; u < p.units; u += gridDim.x * 64 * kWaves * kHalves)
       if (u >= used) {
         plan[2 + 2 * u] = -1;
         plan[p.ud_off + 8 * u] = -1;
       }
   }
   for (int unit = blockIdx.x; unit < used; unit += gridDim.x) {
-    int b, p0, npages, seq, first, chunks, blk0;
+    int b, p0, npages, seq, first, chunks, blk0, blk1;
     if constexpr (kInlinePlan) {
       // the last live sequence whose first unit is <= unit owns it
       const uint64_t own = __ballot(lane < p.batch && wplan[1][lane] > 0 && wplan[0][lane] <= unit);
@@ -620,6 +633,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       npages = min(uniform(wplan[3][b]), p0 + ppc) - p0;
       const int bt0 = b * (int)p.bt_stride + p0;  // (bt_lds: < batch x bt_stride <= kBtLds)
       blk0 = uniform(bt_lds ? bt_s[bt0] : p.block_table[(int64_t)b * p.bt_stride + p0]);
+      blk1 = npages > 1 ? uniform(bt_lds ? bt_s[bt0 + 1] : p.block_table[(int64_t)b * p.bt_stride + p0 + 1]) : 0;
       if (h == 0 && threadIdx.x == 0) {
         // this unit's plan entries for later calls
         int32_t* plan = p.plan;
@@ -627,15 +641,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         plan[3 + 2 * unit] = p0;
         int4* ud = reinterpret_cast<int4*>(plan + p.ud_off + 8 * unit);
         ud[0] = make_int4(b, p0, npages, seq);
-        ud[1] = make_int4(first, chunks, blk0,
-                          npages > 1 ? (bt_lds ? bt_s[bt0 + 1] : p.block_table[(int64_t)b * p.bt_stride + p0 + 1]) : 0);
+        ud[1] = make_int4(first, chunks, blk0, blk1);
       }
     } else {
       // unit descriptor: b, first page, pages, context, first unit of b,
       // chunks of b, block of page 0 (both halves loaded together)
       const int4* udp = reinterpret_cast<const int4*>(p.plan + p.ud_off + 8 * unit);
       const int4 u0 = udp[0], u1 = udp[1];
-      asm volatile("" ::"v"(u0.x), "v"(u0.y), "v"(u0.z), "v"(u0.w), "v"(u1.x), "v"(u1.y), "v"(u1.z));  // one hop
+      asm volatile("" ::"v"(u0.x), "v"(u0.y), "v"(u0.z), "v"(u0.w), "v"(u1.x), "v"(u1.y), "v"(u1.z), "v"(u1.w));  // one hop
       b = uniform(u0.x);
       if (b < 0) continue;
       p0 = uniform(u0.y);
@@ -644,7 +657,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       first = uniform(u1.x);
       chunks = uniform(u1.y);
       blk0 = uniform(u1.z);
+      blk1 = uniform(u1.w);
     }
+    // a two-half workgroup: half 1 starts at page 1 (with a single page it
+    // runs page 0 with every key masked)
+    const int ipage0 = kHalves == 2 ? min(half, npages - 1) : 0;
+    const int blkf = ipage0 == 1 ? blk1 : blk0;
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride + p0;
     // Q rows of the group, issued first so they overlap the record-table
     // hop: wave 0 loads 16-byte pieces L = lane, lane + 64 (row L / 16, u32
@@ -663,7 +681,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                                           : load_block(bt, 0, npages, lane);
     RecRef kr, vr;
     {
-      const int64_t kidx = ((int64_t)blk0 * 2) * p.kvh + h;
+      const int64_t kidx = ((int64_t)blkf * 2) * p.kvh + h;
       const int64_t ka = p.rec_addr[kidx], va = p.rec_addr[kidx + p.kvh];
       const int kl = p.rec_len[kidx], vl = p.rec_len[kidx + p.kvh];
       asm volatile("" ::"v"(ka), "v"(va), "v"(kl), "v"(vl));  // all four in one hop
@@ -704,34 +722,44 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
     expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
     expand_var(vr, vv, w, lane, vlut.s, sh.esc[0][1], sh.hdr[0][1]);
-    // page 1's variable regions: each page's are in flight a page before
-    // they are expanded
+    // the next page's variable regions: each page's are in flight a page
+    // before they are expanded
     RecRef nkr = kr, nvr = vr;
-    if (npages > 1) {
-      nkr = page_ref(meta, 1, 0);
-      nvr = page_ref(meta, 1, 1);
+    const bool second = half + kHalves < npages;
+    if (second) {
+      nkr = page_ref(meta, half + kHalves, 0);
+      nvr = page_ref(meta, half + kHalves, 1);
     }
     __syncthreads();
     patch_raw(kr, vk, w, lane, sh.esc[0][0], sh.hdr[0][0]);
     patch_raw(vr, vv, w, lane, sh.esc[0][1], sh.hdr[0][1]);
-    if (npages > 1) {
+    if (second) {
       vk = prefetch_var(nkr, w, lane);
       vv = prefetch_var(nvr, w, lane);
     }
 
-    for (int i = 0; i < npages; ++i) {
-      const int par = i & 1;
-      const bool more = i + 1 < npages, more2 = i + 2 < npages;
+    // a half takes pages half, half + 2, ...; both halves run the same
+    // number of steps (and barriers): a step past a half's pages repeats its
+    // last page with every key masked
+    const int nsteps = kHalves == 2 ? (npages + 1) >> 1 : npages;
+    for (int j = 0; j < nsteps; ++j) {
+      const int i = kHalves == 2 ? min(2 * j + half, npages - 1) : j;  // page of the unit
+      const bool act = kHalves == 1 || 2 * j + half < npages;
+      const int seq_m = act ? seq : 0;  // context this step's keys are masked against
+      const int par = j & 1;
+      const bool more = act && i + kHalves < npages, more2 = act && i + 2 * kHalves < npages;
       const int tok0 = (p0 + i) * kTokens;
-      if (more2 && ((i + 2) & 63) == 0) meta = load_meta(p, load_block(bt, i + 2, npages, lane), h);
+      // the page after next starts a new window of 64 block ids
+      if (more2 && ((i + 2 * kHalves) & 63) < kHalves)
+        meta = load_meta(p, load_block(bt, (i + 2 * kHalves) & ~63, npages, lane), h);
       // V slab of this page in flight while K is decoded; the variable
       // regions of the page after next in flight for a whole page
       prefetch_dense(vr, w, nt, fv);
       RecRef nnkr = nkr, nnvr = nvr;
       uint2 vk2 = make_uint2(0u, 0u), vv2 = make_uint2(0u, 0u);
       if (more2) {
-        nnkr = page_ref(meta, i + 2, 0);
-        nnvr = page_ref(meta, i + 2, 1);
+        nnkr = page_ref(meta, i + 2 * kHalves, 0);
+        nnvr = page_ref(meta, i + 2 * kHalves, 1);
         vk2 = prefetch_var(nnkr, w, lane);
         vv2 = prefetch_var(nnvr, w, lane);
       }
@@ -739,21 +767,24 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      decode_slab<true>(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0], sh.qt, n, c,
-                  [&](auto, const uint4& w0, const uint4& w1, const uint4& qa) {
-                    s0 = mfma(a_frag(w0, w1, 0), qa, s0);
-                    s1 = mfma(a_frag(w0, w1, 1), qa, s1);
-                  });
+      // (a step past the half's pages decodes nothing: its keys are masked
+      // and its V pass is skipped, so no stale escape data reaches O)
+      if (act)
+        decode_slab<true>(kr, fk, w, nt, np, klut, sh.esc[par][0], sh.hdr[par][0], sh.qt, n, c,
+                    [&](auto, const uint4& w0, const uint4& w1, const uint4& qa) {
+                      s0 = mfma(a_frag(w0, w1, 0), qa, s0);
+                      s1 = mfma(a_frag(w0, w1, 1), qa, s1);
+                    });
       // token of s_j[r] = 32 w + 16 (c >> 1) + 8 j + 4 (c & 1) + r
       // Scores stay unscaled (scale > 0 keeps their order; P = exp2(s c - m c)
       // is one FMA and one exp); the page past the context is masked in a
       // wave-uniform branch.
-      if (tok0 + kTokens > seq) {
+      if (tok0 + kTokens > seq_m) {
         const int tb = tok0 + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if (tb + r >= seq) s0[r] = -INFINITY;
-          if (tb + 8 + r >= seq) s1[r] = -INFINITY;
+          if (tb + r >= seq_m) s0[r] = -INFINITY;
+          if (tb + 8 + r >= seq_m) s1[r] = -INFINITY;
         }
       }
       float mloc = -INFINITY;
@@ -761,6 +792,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
       mloc = xor32_max(xor16_max(mloc));
       if (lane < 8) sh.red[w][lane] = mloc;
+      if (kHalves == 2 && w == 0 && lane < 8) sh.mrun[lane] = m_run;
       // Softmax against the running max m_run, speculatively: the page max is
       // known only after the barrier.  P = exp2((s - m_run) c) stays exact
       // while the page max exceeds m_run by at most kLazyMax / c (P <= 2^kLazyMax);
@@ -798,16 +830,28 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       }
       __syncthreads();  // B2: page max per wave known; P tile written; next page's escapes expanded
       const float mpage = fmaxf(fmaxf(sh.red[0][n & 7], sh.red[1][n & 7]), fmaxf(sh.red[2][n & 7], sh.red[3][n & 7]));
-      // the same decision in every wave: all read the same page maxima
-      if (!spec || __ballot(mpage > m_run + lazy) != 0) {
-        const float m_new = fmaxf(m_run, mpage);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.scale_log2);
-        m_run = m_new;
-        l_run *= alpha;
-        o0 *= alpha;
-        o1 *= alpha;
-        softmax_tile(m_use);
+      // the same decision in every wave: all read the same page maxima (and
+      // in a two-half workgroup, each half also works out the other's, so
+      // that both meet the extra barrier together)
+      const bool renorm = !spec || __ballot(mpage > m_run + lazy) != 0;
+      bool extra = renorm;
+      if constexpr (kHalves == 2) {
+        const AttnShared& ot = shs[half ^ 1];
+        const float mp_o = fmaxf(fmaxf(ot.red[0][n & 7], ot.red[1][n & 7]), fmaxf(ot.red[2][n & 7], ot.red[3][n & 7]));
+        const float mr_o = ot.mrun[n & 7];
+        extra = extra || mr_o == -INFINITY || __ballot(mp_o > mr_o + lazy) != 0;
+      }
+      if (extra) {
+        if (renorm) {
+          const float m_new = fmaxf(m_run, mpage);
+          const float m_use = m_new == -INFINITY ? 0.f : m_new;
+          const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.scale_log2);
+          m_run = m_new;
+          l_run *= alpha;
+          o0 *= alpha;
+          o1 *= alpha;
+          softmax_tile(m_use);
+        }
         __syncthreads();  // rewritten P tile complete
       }
       l_run += psum;
@@ -817,11 +861,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       }
 
       // ---- O^T += V^T P^T for dims 32w .. 32w + 31 ----
-      decode_slab<true>(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
-                  [&](auto, const uint4& w0, const uint4& w1, const uint4& pa) {
-                    o0 = mfma(a_frag(w0, w1, 0), pa, o0);
-                    o1 = mfma(a_frag(w0, w1, 1), pa, o1);
-                  });
+      if (act)
+        decode_slab<true>(vr, fv, w, nt, np, vlut, sh.esc[par][1], sh.hdr[par][1], sh.pt, n, c,
+                    [&](auto, const uint4& w0, const uint4& w1, const uint4& pa) {
+                      o0 = mfma(a_frag(w0, w1, 0), pa, o0);
+                      o1 = mfma(a_frag(w0, w1, 1), pa, o1);
+                    });
       kr = nkr;
       vr = nvr;
       nkr = nnkr;
@@ -836,10 +881,37 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     __syncthreads();  // everyone is past B2's reads of red
     if (lane < 8) sh.red[w][lane] = l_tot;
     __syncthreads();
-    const float l_all = sh.red[0][n & 7] + sh.red[1][n & 7] + sh.red[2][n & 7] + sh.red[3][n & 7];
+    float l_all = sh.red[0][n & 7] + sh.red[1][n & 7] + sh.red[2][n & 7] + sh.red[3][n & 7];
+    if constexpr (kHalves == 2) {
+      // half 1 hands its (O, m, l) to half 0 through LDS (its escape area,
+      // free now); half 0 merges them into its registers
+      float* xo = reinterpret_cast<float*>(&shs[1].esc[0][0][0]);  // [head 8][dim 128], then m[8], l[8]
+      const int d0 = 32 * w + 16 * (c >> 1) + 4 * (c & 1);
+      if (half == 1 && hh == 0) {
+        *reinterpret_cast<float4*>(xo + n * kDim + d0) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+        *reinterpret_cast<float4*>(xo + n * kDim + d0 + 8) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+        if (w == 0 && c == 0) {
+          xo[8 * kDim + n] = m_run;
+          xo[8 * kDim + 8 + n] = l_all;
+        }
+      }
+      __syncthreads();
+      if (half == 0) {
+        const float m1 = xo[8 * kDim + (n & 7)], l1 = xo[8 * kDim + 8 + (n & 7)];
+        const float m_new = fmaxf(m_run, m1);
+        const float a0 = __builtin_amdgcn_exp2f((m_run - m_new) * p.scale_log2);
+        const float a1 = __builtin_amdgcn_exp2f((m1 - m_new) * p.scale_log2);
+        const float4 x0 = *reinterpret_cast<const float4*>(xo + (n & 7) * kDim + d0);
+        const float4 x1 = *reinterpret_cast<const float4*>(xo + (n & 7) * kDim + d0 + 8);
+        o0 = o0 * a0 + f32x4{x0.x, x0.y, x0.z, x0.w} * a1;
+        o1 = o1 * a0 + f32x4{x1.x, x1.y, x1.z, x1.w} * a1;
+        l_all = l_all * a0 + l1 * a1;
+        m_run = m_new;
+      }
+    }
     if (chunks == 1) {
       // the whole sequence in one unit: normalise and write the output rows
-      if (hh == 0 && n < p.group) {
+      if (half == 0 && hh == 0 && n < p.group) {
         const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
         auto pk = pack_bf16x2;
         uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.group + n) * kDim + 32 * w +
@@ -850,18 +922,18 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       continue;
     }
     const int64_t row = ((int64_t)h * p.units + unit) * 8 + n;
-    if (hh == 0) {
+    if (half == 0 && hh == 0) {
       const rsrc_t ro = coh_rsrc(p.opart);
       const int64_t i0 = row * kDim + 32 * w + 16 * (c >> 1) + 4 * (c & 1);
       st_coh4(ro, i0, o0[0], o0[1], o0[2], o0[3]);
       st_coh4(ro, i0 + 8, o1[0], o1[1], o1[2], o1[3]);
       if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run * p.scale_log2, l_all);
     }
-    merge_chunks(p, sh, b, h, first, chunks);
+    merge_chunks(p, shs[0], b, h, first, chunks);
   }
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
-    for (int b = w; b < p.batch; b += kWaves) {
+    for (int b = wave; b < p.batch; b += kWaves * kHalves) {
       const int cnt = kInlinePlan ? wplan[1][b] : p.plan[3 + 2 * p.units + 2 * b];
       if (cnt != 0) continue;
       uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)h * p.group * kDim);
@@ -875,16 +947,15 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
 using namespace fp;
 
-// Workgroups of attn_kernel resident on the current device at once:
-// kAttnPerCu per compute unit (cached per device).
-static int decode_slots() {
+// Compute units of the current device (cached per device).
+static int device_cus() {
   static int cache[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (cache[dev] == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev] = kAttnPerCu * cus;
+    cache[dev] = cus;
   }
   return cache[dev];
 }
@@ -933,9 +1004,14 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   p.ud_off = ud_offset((int)units);
   p.done = plan + plan_elems - units * kv_heads;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
-  const int slots = decode_slots();
-  FP_CHECK(slots > 0, "cannot query the device's compute-unit count");
+  const int cus = device_cus();
+  FP_CHECK(cus > 0, "cannot query the device's compute-unit count");
+  // resident workgroups: kAttnPerCu 4-wave ones per CU, or one two-half
+  // (8-wave) workgroup per CU for launches with few (sequence, head) pairs
+  const int halves = batch * kv_heads <= kHalvesPairs ? 2 : 1;
+  const int slots = halves == 2 ? cus : kAttnPerCu * cus;
   p.slots = slots;
+  p.halves = halves;
   // replan 2 / 3: plan inside the attention kernel (batch <= 64; the merge
   // counters must be as a previous completed call left them, i.e. zero)
   FP_CHECK(replan >= 0 && replan <= 3, "replan must be 0, 1, 2 or 3");
@@ -943,17 +1019,23 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   p.bt_lds = replan == 3 && p.inline_plan && batch * bt_stride <= kBtLds;
   if (replan && !p.inline_plan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
-                       plan_elems, (int)batch, (int)units, (int)kv_heads, slots);
+                       plan_elems, (int)batch, (int)units, (int)kv_heads, slots, halves);
     FP_LAUNCH_CHECK();
   }
   // persistent grid: one resident wave of workgroups (slots over all KV
   // heads) walks the units in use
   const int64_t per_head = std::min<int64_t>(units, (slots + kv_heads - 1) / kv_heads);
-  const dim3 grid((unsigned)per_head, (unsigned)kv_heads), block(64 * kWaves);
-  if (p.inline_plan)
-    hipLaunchKernelGGL((attn_kernel<true>), grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL((attn_kernel<false>), grid, block, 0, stream, p);
+  const dim3 grid((unsigned)per_head, (unsigned)kv_heads), block(64 * kWaves * halves);
+  if (halves == 2) {
+    if (p.inline_plan)
+      hipLaunchKernelGGL((attn_kernel<true, 2>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((attn_kernel<false, 2>), grid, block, 0, stream, p);
+  } else if (p.inline_plan) {
+    hipLaunchKernelGGL((attn_kernel<true, 1>), grid, block, 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((attn_kernel<false, 1>), grid, block, 0, stream, p);
+  }
   FP_LAUNCH_CHECK();
   return 0;
 }
