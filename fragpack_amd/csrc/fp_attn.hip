@@ -555,8 +555,10 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
       make_uint2(lo, hi);
 }
 
+// (a two-half workgroup runs alone on its CU, two waves per SIMD: it may use
+// the whole 256-register budget)
 template <bool kInlinePlan, int kHalves>
-__global__ void __launch_bounds__(64 * kWaves * kHalves) __attribute__((amdgpu_waves_per_eu(kAttnPerCu)))
+__global__ void __launch_bounds__(64 * kWaves * kHalves) __attribute__((amdgpu_waves_per_eu(kHalves == 2 ? 2 : kAttnPerCu)))
 attn_kernel(AttnParams p) {
   __shared__ AttnShared shs[kHalves];
   const int lane = wave_lane();
