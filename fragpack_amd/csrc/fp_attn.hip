@@ -474,8 +474,10 @@ __device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane)
   for (int b = 0; b < p.batch; ++b) chunks += dv.chunks(__builtin_amdgcn_readlane(r.n, b));
   uint64_t key = ~0ull;
   if (chunks <= p.units) {
-    const int64_t rounds = ((int64_t)chunks * p.kvh + p.slots - 1) / p.slots;
-    key = ((uint64_t)(rounds * ((cand + p.halves - 1) / p.halves + kUnitCost)) << 24) | (uint64_t)(0xFFFFFF - cand);
+    // (chunks * kvh + slots < 2^24 for an inline-planning launch: Divider's range)
+    const int rounds = Divider(p.slots).div(chunks * p.kvh + p.slots - 1);
+    key = ((uint64_t)(rounds * ((cand + p.halves - 1) >> (p.halves - 1)) + rounds * kUnitCost) << 24) |
+          (uint64_t)(0xFFFFFF - cand);
   }
   key = wave_min_u64(key);
   r.ppc = uniform(0xFFFFFF - (int)(key & 0xFFFFFFu));
@@ -601,27 +603,6 @@ attn_kernel(AttnParams p) {
     // reads for the compiler too (the wave's LDS accesses are in order)
     wave_lds_sync();
   }
-  if (kInlinePlan && blockIdx.x == 0 && h == 0 && wave == 0) {
-    // the plan words for later calls that reuse this plan
-    int32_t* plan = p.plan;
-    if (lane < p.batch) {
-      plan[2 + 2 * p.units + 2 * lane] = ip.first;
-      plan[3 + 2 * p.units + 2 * lane] = ip.cnt;
-    }
-    if (lane == 0) {
-      plan[0] = ip.ppc;
-      plan[1] = ip.used;
-    }
-  }
-  if (kInlinePlan && h == 0) {
-    // idle units of this workgroup's stride
-    int32_t* plan = p.plan;
-    for (int u = blockIdx.x + gridDim.x * (int)threadIdx.x; u < p.units; u += gridDim.x * 64 * kWaves * kHalves)
-      if (u >= used) {
-        plan[2 + 2 * u] = -1;
-        plan[p.ud_off + 8 * u] = -1;
-      }
-  }
   for (int unit = blockIdx.x; unit < used; unit += gridDim.x) {
     int b, p0, npages, seq, first, chunks, blk0, blk1;
     if constexpr (kInlinePlan) {
@@ -633,17 +614,18 @@ attn_kernel(AttnParams p) {
       seq = uniform(wplan[2][b]);
       p0 = (unit - first) * ppc;
       npages = min(uniform(wplan[3][b]), p0 + ppc) - p0;
-      const int bt0 = b * (int)p.bt_stride + p0;  // (bt_lds: < batch x bt_stride <= kBtLds)
-      blk0 = uniform(bt_lds ? bt_s[bt0] : p.block_table[(int64_t)b * p.bt_stride + p0]);
-      blk1 = npages > 1 ? uniform(bt_lds ? bt_s[bt0 + 1] : p.block_table[(int64_t)b * p.bt_stride + p0 + 1]) : 0;
-      if (h == 0 && threadIdx.x == 0) {
-        // this unit's plan entries for later calls
-        int32_t* plan = p.plan;
-        plan[2 + 2 * unit] = b;
-        plan[3 + 2 * unit] = p0;
-        int4* ud = reinterpret_cast<int4*>(plan + p.ud_off + 8 * unit);
-        ud[0] = make_int4(b, p0, npages, seq);
-        ud[1] = make_int4(first, chunks, blk0, blk1);
+      // the first two block ids: LDS and global reads in separate branches
+      // (one read through a generic pointer would be a flat load, whose
+      // wait also waits for every store in flight)
+      if (bt_lds) {
+        const int bt0 = b * (int)p.bt_stride + p0;  // < batch x bt_stride <= kBtLds
+        blk0 = uniform(bt_s[bt0]);
+        blk1 = npages > 1 ? uniform(bt_s[bt0 + 1]) : 0;
+      } else {
+        asm volatile("" ::: "memory");
+        const int32_t* row = p.block_table + (int64_t)b * p.bt_stride + p0;
+        blk0 = uniform(row[0]);
+        blk1 = npages > 1 ? uniform(row[1]) : 0;
       }
     } else {
       // unit descriptor: b, first page, pages, context, first unit of b,
@@ -884,6 +866,16 @@ attn_kernel(AttnParams p) {
     if (lane < 8) sh.red[w][lane] = l_tot;
     __syncthreads();
     float l_all = sh.red[0][n & 7] + sh.red[1][n & 7] + sh.red[2][n & 7] + sh.red[3][n & 7];
+    if (kInlinePlan && h == 0 && threadIdx.x == 0) {
+      // this unit's plan entries for later calls (stored after the page loop:
+      // the first waits for loads would otherwise also wait for these stores)
+      int32_t* plan = p.plan;
+      plan[2 + 2 * unit] = b;
+      plan[3 + 2 * unit] = p0;
+      int4* ud = reinterpret_cast<int4*>(plan + p.ud_off + 8 * unit);
+      ud[0] = make_int4(b, p0, npages, seq);
+      ud[1] = make_int4(first, chunks, blk0, blk1);
+    }
     if constexpr (kHalves == 2) {
       // half 1 hands its (O, m, l) to half 0 through LDS (its escape area,
       // free now); half 0 merges them into its registers
@@ -932,6 +924,28 @@ attn_kernel(AttnParams p) {
       if (w == 0 && c == 0) st_coh2(coh_rsrc(p.ml), row * 2, m_run * p.scale_log2, l_all);
     }
     merge_chunks(p, shs[0], b, h, first, chunks);
+  }
+  // the plan words for later calls that reuse this plan (at the end, after
+  // every load of the kernel)
+  if (kInlinePlan && blockIdx.x == 0 && h == 0 && wave == 0) {
+    int32_t* plan = p.plan;
+    if (lane < p.batch) {
+      plan[2 + 2 * p.units + 2 * lane] = ip.first;
+      plan[3 + 2 * p.units + 2 * lane] = ip.cnt;
+    }
+    if (lane == 0) {
+      plan[0] = ip.ppc;
+      plan[1] = ip.used;
+    }
+  }
+  if (kInlinePlan && h == 0) {
+    // idle units of this workgroup's stride
+    int32_t* plan = p.plan;
+    for (int u = blockIdx.x + gridDim.x * (int)threadIdx.x; u < p.units; u += gridDim.x * 64 * kWaves * kHalves)
+      if (u >= used) {
+        plan[2 + 2 * u] = -1;
+        plan[p.ud_off + 8 * u] = -1;
+      }
   }
   // rows with no context produce zeros (workgroup 0 of each head)
   if (blockIdx.x == 0) {
@@ -1017,7 +1031,7 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   // replan 2 / 3: plan inside the attention kernel (batch <= 64; the merge
   // counters must be as a previous completed call left them, i.e. zero)
   FP_CHECK(replan >= 0 && replan <= 3, "replan must be 0, 1, 2 or 3");
-  p.inline_plan = (replan == 2 || replan == 3) && batch <= 64;
+  p.inline_plan = (replan == 2 || replan == 3) && batch <= 64 && units * kv_heads + slots < (1 << 24);
   p.bt_lds = replan == 3 && p.inline_plan && batch * bt_stride <= kBtLds;
   if (replan && !p.inline_plan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
