@@ -315,7 +315,7 @@ __device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt
 __device__ __forceinline__ bool quarter_used(const RecRef& r, int w) { return r.vlen <= kVarCap && 512 * w < r.vlen; }
 
 __device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane) {
-  return quarter_used(r, w) ? bld8(r.rs(), 8 * lane, kDenseBytes + 512 * w) : make_uint2(0u, 0u);
+  return quarter_used(r, w) ? rld8(r.rs(), 8 * lane, kDenseBytes + 512 * w) : make_uint2(0u, 0u);
 }
 
 // Per-record escape staging, done by all four waves from their prefetched

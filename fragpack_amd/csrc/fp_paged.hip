@@ -93,7 +93,8 @@ struct KFrag {
   uint4 k[2][4];  // [16-key tile][k-step]: key 16 t + j, dims 32 ks + 8 q4 .. + 7
 };
 
-// A block id outside the caches reads as an empty page (zero-sized
+// Pages are streamed with the non-temporal load policy, as the compressed
+// kernel streams its records.  A block id outside the caches reads as an empty page (zero-sized
 // resources: every load returns zero) and the caller masks all its keys;
 // returns whether the page is inside.
 __device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int h, int w, int valid, int lane,
@@ -110,7 +111,7 @@ __device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int
   for (int t = 0; t < 2; ++t) {
     const int key = min(kPgWaveKeys * w + 16 * t + j, valid - 1);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kf.k[t][ks] = bld16(rk, key * row + 64 * ks + 16 * q4, 0);
+    for (int ks = 0; ks < 4; ++ks) kf.k[t][ks] = rld16(rk, key * row + 64 * ks + 16 * q4, 0);
   }
   // V: each instruction fills 1 KB of the stage (four rows), lane L slot L % 16
   // of row L / 16, i.e. chunk (L % 16) ^ (row & 15)
@@ -119,7 +120,7 @@ __device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int
     const int r = 4 * i + (lane >> 4);
     const int key = min(kPgWaveKeys * w + r, valid - 1);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pg_lds_ptr_t)(vstage + 4 * i * kPgRow), 16,
-                                             key * row + 16 * ((lane & 15) ^ (r & 15)), 0, 0, 0);
+                                             key * row + 16 * ((lane & 15) ^ (r & 15)), 0, 0, kNt);
   }
   return inside;
 }
