@@ -825,6 +825,18 @@ __device__ __forceinline__ void enc_var(const uint4 (&wd)[8], const uint32_t (&c
   lds_barrier();
 }
 
+// Streaming stores (the non-temporal policy: a record is written once and
+// read by a later launch).
+// (through the global address space: a generic pointer would make flat
+// stores, which every later LDS wait would also wait for)
+__device__ __forceinline__ void st16_nt(uint8_t* p, uint4 v) {
+  const u32x4_t x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<FP_GLOBAL u32x4_t*>(reinterpret_cast<uintptr_t>(p)));
+}
+__device__ __forceinline__ void st8_nt(uint8_t* p, uint32_t a, uint32_t b) {
+  __builtin_nontemporal_store(u32x2_t{a, b}, reinterpret_cast<FP_GLOBAL u32x2_t*>(reinterpret_cast<uintptr_t>(p)));
+}
+
 // Writes a coded record (dense part from registers, variable part from LDS)
 // at ``dst`` (16-byte aligned).
 __device__ __forceinline__ void enc_store(uint8_t* dst, const uint4 (&wd)[8], const uint32_t (&sym)[6],
@@ -834,15 +846,13 @@ __device__ __forceinline__ void enc_store(uint8_t* dst, const uint4 (&wd)[8], co
   for (int j = 0; j < 4; ++j) {
     const uint4 a = wd[2 * j], c = wd[2 * j + 1];
     // low bytes of the 16 scalars of chunk j
-    *reinterpret_cast<uint4*>(dst + 16 * (256 * j + tid)) =
-        make_uint4(perm(a.y, a.x, 0x06040200u), perm(a.w, a.z, 0x06040200u), perm(c.y, c.x, 0x06040200u),
-                   perm(c.w, c.z, 0x06040200u));
+    st16_nt(dst + 16 * (256 * j + tid), make_uint4(perm(a.y, a.x, 0x06040200u), perm(a.w, a.z, 0x06040200u),
+                                                   perm(c.y, c.x, 0x06040200u), perm(c.w, c.z, 0x06040200u)));
   }
 #pragma unroll
-  for (int m = 0; m < 3; ++m)
-    *reinterpret_cast<uint2*>(dst + kLowBytes + 8 * (256 * m + tid)) = make_uint2(sym[2 * m], sym[2 * m + 1]);
+  for (int m = 0; m < 3; ++m) st8_nt(dst + kLowBytes + 8 * (256 * m + tid), sym[2 * m], sym[2 * m + 1]);
   for (int i = tid; i < var_len / 16; i += kThreads)
-    *reinterpret_cast<uint4*>(dst + kDenseBytes + 16 * i) = reinterpret_cast<const uint4*>(sh.var32)[i];
+    st16_nt(dst + kDenseBytes + 16 * i, reinterpret_cast<const uint4*>(sh.var32)[i]);
 }
 
 // Persistent encoder: workgroup g encodes records r = g, g + grid, ... of
@@ -865,7 +875,7 @@ __device__ __forceinline__ void stage_record(EncStage& st_buf, const uint8_t* sr
 #pragma unroll
   for (int st = 0; st < 8; ++st)
     __builtin_amdgcn_global_load_lds((gptr_t)(src + 16 * (256 * st + tid)), (lptr_t)&st_buf.w[st][64 * wave], 16, 0,
-                                     0);
+                                     kNt);
 }
 
 
@@ -1089,7 +1099,7 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       if (slot >= 0) {  // else the record stays in staging (data loss is counted)
         uint8_t* dst = s.ovf_base + (int64_t)slot * kRawRecord;
 #pragma unroll
-        for (int st = 0; st < 8; ++st) *reinterpret_cast<uint4*>(dst + 16 * (256 * st + tid)) = wd[st];
+        for (int st = 0; st < 8; ++st) st16_nt(dst + 16 * (256 * st + tid), wd[st]);
         if (tid == 0) {
           s.rec_addr[idx] = reinterpret_cast<int64_t>(dst);
           s.rec_len[idx] = kRawVarLen;
