@@ -168,6 +168,15 @@ __device__ __forceinline__ uint2 ld8(const uint8_t* p) {
 __device__ __forceinline__ uint32_t ld4(const uint8_t* p) {
   return *reinterpret_cast<const FP_GLOBAL uint32_t*>(reinterpret_cast<uintptr_t>(p));
 }
+// The same with the non-temporal policy, for record data read once.
+__device__ __forceinline__ uint4 ld16_nt(const uint8_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const FP_GLOBAL u32x4_t*>(reinterpret_cast<uintptr_t>(p)));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8_nt(const uint8_t* p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const FP_GLOBAL u32x2_t*>(reinterpret_cast<uintptr_t>(p)));
+  return make_uint2(v.x, v.y);
+}
 
 // Buffer-resource loads: a wave-uniform record base in SGPRs, a per-lane
 // 32-bit byte offset and a wave-uniform SGPR offset; out-of-range reads
@@ -252,13 +261,13 @@ __device__ __forceinline__ void load_slab(rsrc_t r, bool raw, int slab, int nt, 
 __device__ __forceinline__ void load_thread(const uint8_t* rec, bool raw, int t, SlabBuf& b) {
   if (raw) {
 #pragma unroll
-    for (int st = 0; st < 6; ++st) b.v[st] = ld16(rec + 16 * (256 * st + t));
+    for (int st = 0; st < 6; ++st) b.v[st] = ld16_nt(rec + 16 * (256 * st + t));
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b.v[j] = ld16(rec + 16 * (256 * j + t));
-    const uint2 s0 = ld8(rec + kLowBytes + 8 * t);
-    const uint2 s1 = ld8(rec + kLowBytes + 8 * (256 + t));
-    const uint2 s2 = ld8(rec + kLowBytes + 8 * (512 + t));
+    for (int j = 0; j < 4; ++j) b.v[j] = ld16_nt(rec + 16 * (256 * j + t));
+    const uint2 s0 = ld8_nt(rec + kLowBytes + 8 * t);
+    const uint2 s1 = ld8_nt(rec + kLowBytes + 8 * (256 + t));
+    const uint2 s2 = ld8_nt(rec + kLowBytes + 8 * (512 + t));
     b.v[4] = make_uint4(s0.x, s0.y, s1.x, s1.y);
     b.v[5] = make_uint4(s2.x, s2.y, 0u, 0u);
   }
@@ -423,7 +432,7 @@ __device__ __forceinline__ int thread_escapes(const SlabBuf& b) {
 // read here.
 template <typename Emit>
 __device__ __forceinline__ void raw_words(const SlabBuf& b, const uint8_t* rec, int t, Emit&& emit) {
-  const uint4 w6 = ld16(rec + 16 * (256 * 6 + t)), w7 = ld16(rec + 16 * (256 * 7 + t));
+  const uint4 w6 = ld16_nt(rec + 16 * (256 * 6 + t)), w7 = ld16_nt(rec + 16 * (256 * 7 + t));
   static_for<0, 6>([&](auto st) { emit(st, b.v[st]); });
   emit(std::integral_constant<int, 6>{}, w6);
   emit(std::integral_constant<int, 7>{}, w7);

@@ -1209,7 +1209,7 @@ __device__ __forceinline__ void store_tile(const DecShared& sh, uint8_t* out, in
   for (int q = 0; q < 8; ++q) {
     const int x = q * kThreads + threadIdx.x, r = x >> 4, jj = x & 15;
     const uint4 val = *reinterpret_cast<const uint4*>(sh.tile + r * kTileRow + (((jj ^ (r & 15)) & 15) << 4));
-    *reinterpret_cast<uint4*>(out + r * row_stride + jj * 16) = val;
+    st16_nt(out + r * row_stride + jj * 16, val);
   }
 }
 
@@ -1337,9 +1337,9 @@ __device__ __forceinline__ void wave_copy_record(uint8_t* dst, const uint8_t* sr
   for (int base = 16 * lane; base < bytes + 16 * lane; base += 1024 * kCopyDepth) {
     u32x4_t v[kCopyDepth];
 #pragma unroll
-    for (int k = 0; k < kCopyDepth; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, base + 1024 * k, 0, 0);
+    for (int k = 0; k < kCopyDepth; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, base + 1024 * k, 0, kNt);
 #pragma unroll
-    for (int k = 0; k < kCopyDepth; ++k) __builtin_amdgcn_raw_buffer_store_b128(v[k], rd, base + 1024 * k, 0, 0);
+    for (int k = 0; k < kCopyDepth; ++k) __builtin_amdgcn_raw_buffer_store_b128(v[k], rd, base + 1024 * k, 0, kNt);
   }
 }
 
