@@ -97,6 +97,7 @@ struct KFrag {
 // kernel streams its records.  A block id outside the caches reads as an empty page (zero-sized
 // resources: every load returns zero) and the caller masks all its keys;
 // returns whether the page is inside.
+template <int kPolicy>
 __device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int h, int w, int valid, int lane,
                                           KFrag& kf, uint8_t* vstage) {
   const int j = lane & 15, q4 = lane >> 4;
@@ -111,7 +112,10 @@ __device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int
   for (int t = 0; t < 2; ++t) {
     const int key = min(kPgWaveKeys * w + 16 * t + j, valid - 1);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kf.k[t][ks] = rld16(rk, key * row + 64 * ks + 16 * q4, 0);
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rk, key * row + 64 * ks + 16 * q4, 0, kPolicy);
+      kf.k[t][ks] = make_uint4(v.x, v.y, v.z, v.w);
+    }
   }
   // V: each instruction fills 1 KB of the stage (four rows), lane L slot L % 16
   // of row L / 16, i.e. chunk (L % 16) ^ (row & 15)
@@ -120,7 +124,7 @@ __device__ __forceinline__ bool load_page(const PagedParams& p, int64_t blk, int
     const int r = 4 * i + (lane >> 4);
     const int key = min(kPgWaveKeys * w + r, valid - 1);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pg_lds_ptr_t)(vstage + 4 * i * kPgRow), 16,
-                                             key * row + 16 * ((lane & 15) ^ (r & 15)), 0, 0, kNt);
+                                             key * row + 16 * ((lane & 15) ^ (r & 15)), 0, 0, kPolicy);
   }
   return inside;
 }
@@ -199,6 +203,7 @@ static_assert(sizeof(CombineShared) <= kPgWaves * kPgStage, "combine reuses the 
 
 constexpr int kPgMergeBatch = 16;
 
+template <int kPolicy>
 __global__ void __launch_bounds__(kPgThreads) __attribute__((amdgpu_waves_per_eu(kPgPerCu)))
 paged_decode_kernel(PagedParams p) {
   // The two V stages are separate LDS objects, named statically in the
@@ -233,10 +238,10 @@ paged_decode_kernel(PagedParams p) {
   if (pg0 < pg1) {
     KFrag ka, kb;
     auto valid_of = [&](int pg) { return min(128, len - pg * 128); };
-    bool in_a = load_page(p, bt[pg0], h, w, valid_of(pg0), lane, ka, stage0[w]), in_b = false;
+    bool in_a = load_page<kPolicy>(p, bt[pg0], h, w, valid_of(pg0), lane, ka, stage0[w]), in_b = false;
     // two pages per trip so that each stage and fragment set is named statically
     for (int pg = pg0; pg < pg1; pg += 2) {
-      if (pg + 1 < pg1) in_b = load_page(p, bt[pg + 1], h, w, valid_of(pg + 1), lane, kb, stage1[w]);
+      if (pg + 1 < pg1) in_b = load_page<kPolicy>(p, bt[pg + 1], h, w, valid_of(pg + 1), lane, kb, stage1[w]);
       // page pg landed: only the next page's 16 transfers may still be in flight
       if (pg + 1 < pg1)
         __builtin_amdgcn_s_waitcnt(kVmcnt16);
@@ -244,7 +249,7 @@ paged_decode_kernel(PagedParams p) {
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
       page_step(p, qf, ka, stage0[w], pg * 128 + kPgWaveKeys * w, in_a ? len : 0, lane, st);
       if (pg + 1 >= pg1) break;
-      if (pg + 2 < pg1) in_a = load_page(p, bt[pg + 2], h, w, valid_of(pg + 2), lane, ka, stage0[w]);
+      if (pg + 2 < pg1) in_a = load_page<kPolicy>(p, bt[pg + 2], h, w, valid_of(pg + 2), lane, ka, stage0[w]);
       if (pg + 2 < pg1)
         __builtin_amdgcn_s_waitcnt(kVmcnt16);
       else
@@ -355,6 +360,18 @@ paged_decode_kernel(PagedParams p) {
 
 using namespace fp;
 
+// Load policy of the paged kernel's K and V page loads: non-temporal
+// (default) or plain.  Which is faster depends on the shape (measured: the
+// non-temporal policy is faster at batch 4 x 8K, slower at 16 x 32 heads
+// ragged), so a baseline measurement tries both.  Process-wide; not for
+// concurrent callers.
+static int g_paged_streaming = 1;
+
+extern "C" int fp_paged_set_streaming(int on) {
+  g_paged_streaming = on ? 1 : 0;
+  return 0;
+}
+
 extern "C" int fp_paged_decode_splits(int64_t batch, int64_t kv_heads, int64_t max_seq_len) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -416,8 +433,11 @@ extern "C" int fp_paged_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.splits = (int)splits;
   p.ppc = (int)((pages + splits - 1) / splits);
   p.scale_log2 = (float)(scale * 1.4426950408889634);
-  hipLaunchKernelGGL(paged_decode_kernel, dim3((unsigned)splits, (unsigned)kv_heads, (unsigned)batch),
-                     dim3(kPgThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
+  const dim3 grid((unsigned)splits, (unsigned)kv_heads, (unsigned)batch);
+  if (g_paged_streaming)
+    hipLaunchKernelGGL(paged_decode_kernel<kNt>, grid, dim3(kPgThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
+  else
+    hipLaunchKernelGGL(paged_decode_kernel<0>, grid, dim3(kPgThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
   FP_LAUNCH_CHECK();
   return 0;
 }

@@ -125,6 +125,7 @@ class Extension:
             "fp_paged_decode": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p,
                                 _i64, _p, _i64, _p, _i64, _f64, _p],
             "fp_paged_decode_splits": [_i64, _i64, _i64],
+            "fp_paged_set_streaming": [_i32],
             "fp_prefill_attention": [_p, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _f64,
                                      _i32, _p, _i64, _p],
         }
@@ -330,6 +331,9 @@ class Extension:
     # -- plain BF16 paged decode (the baseline arm; the FA3 call of fragpack_step_bench.py:205-284) --
     def paged_decode_splits(self, batch: int, kv_heads: int, max_seq_len: int) -> int:
         return int(self._lib.fp_paged_decode_splits(int(batch), int(kv_heads), int(max_seq_len)))
+
+    def paged_set_streaming(self, on: bool) -> None:
+        self._lib.fp_paged_set_streaming(1 if on else 0)
 
     def paged_decode(self, q, k_cache, v_cache, block_table, seq_lens, max_seq_len: int, splits: int, opart, ml,
                      counters, out, scale: float) -> None:

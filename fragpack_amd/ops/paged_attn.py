@@ -23,6 +23,12 @@ def paged_splits(batch: int, kv_heads: int, max_seq_len: int) -> int:
     return extension().paged_decode_splits(batch, kv_heads, max_seq_len)
 
 
+def set_streaming_loads(on: bool) -> None:
+    """Page loads with the non-temporal policy (default) or plain; which is
+    faster depends on the shape.  Process-wide."""
+    extension().paged_set_streaming(on)
+
+
 def paged_workspace(batch: int, kv_heads: int, splits: int, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """``(opart, ml, counters)`` for :func:`paged_decode_attention`; the
     counters start at zero and every completed call leaves them at zero."""
@@ -53,4 +59,4 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
                              out, scale)
 
 
-__all__ = ["paged_decode_attention", "paged_splits", "paged_workspace"]
+__all__ = ["paged_decode_attention", "paged_splits", "paged_workspace", "set_streaming_loads"]

@@ -148,6 +148,11 @@ int fp_paged_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_h
                     void* out, int64_t out_stride, double scale, fp_stream_t stream);
 /* Splits per (sequence, head) that fill the current device. */
 int fp_paged_decode_splits(int64_t batch, int64_t kv_heads, int64_t max_seq_len);
+/* Load policy of fp_paged_decode's page loads: 1 non-temporal (default), 0
+ * plain.  The faster one depends on the shape, so the baseline is measured
+ * with both.  Process-wide, not for concurrent callers.  No counterpart in
+ * the reference (FA3 chooses its own loads). */
+int fp_paged_set_streaming(int on);
 
 /* Step start: GC, staging claims, close list.  Replaces hbm_prepare
  * (fragpack_ext.cpp:11-17, hbm_kv.cu:669-686). */
