@@ -1352,8 +1352,9 @@ __device__ __forceinline__ int64_t wave_bytes_before(const Size& size, int upto,
   return sum;
 }
 
-// grid (ceil(L * 2H / kExportWaves), n): wave w of workgroup x copies record
-// g = x * kExportWaves + w (layer g / 2H, kv-head g % 2H) of blocks[y]; the
+// grid n x ceil(L * 2H / kExportWaves), blob-major (neighbouring workgroups
+// write neighbouring records): wave w of the blob's workgroup y copies
+// record g = y * kExportWaves + w (layer g / 2H, kv-head g % 2H); the
 // wave of record 0 also writes the header, the length table and the blob's
 // aligned length.
 __global__ void __launch_bounds__(64 * kExportWaves) blob_export_kernel(const int32_t* blocks, const int64_t* rec_addr,
@@ -1361,8 +1362,9 @@ __global__ void __launch_bounds__(64 * kExportWaves) blob_export_kernel(const in
                                                                        int64_t stride, int64_t* lengths, int L, int H,
                                                                        int NB, int64_t digest) {
   const int lane = wave_lane(), w = uniform((int)(threadIdx.x >> 6));
-  const int i = blockIdx.y, per = 2 * H, count = L * per;
-  const int g = (int)blockIdx.x * kExportWaves + w;
+  const int per = 2 * H, count = L * per, groups = (count + kExportWaves - 1) / kExportWaves;
+  const int i = (int)(blockIdx.x / groups);  // blob
+  const int g = (int)(blockIdx.x % groups) * kExportWaves + w;
   const int b = uniform(blocks[i]);
   // table entry of record gg: rec_len[layer][b][kv-head]
   auto entry = [&](int gg) { return ((int64_t)(gg / per) * NB + b) * per + gg % per; };
@@ -1743,8 +1745,9 @@ extern "C" int fp_hbm_export(const int32_t* blocks, int64_t n, const int64_t* re
                out_bytes >= n * stride,
            "export stride or buffer too small");
   const int64_t count = 2 * num_layers * kv_heads;
-  FP_CHECK(n < 65536 && count < (1LL << 24), "too many blobs or records per blob in one export");
-  hipLaunchKernelGGL(blob_export_kernel, dim3((unsigned)((count + kExportWaves - 1) / kExportWaves), (unsigned)n),
+  const int64_t groups = (count + kExportWaves - 1) / kExportWaves;
+  FP_CHECK(n * groups < (1LL << 31), "too many blobs or records per blob in one export");
+  hipLaunchKernelGGL(blob_export_kernel, dim3((unsigned)(n * groups)),
                      dim3(64 * kExportWaves), 0, stream, blocks,
                      rec_addr, rec_len, out, stride, lengths, (int)num_layers, (int)kv_heads, (int)num_blocks, digest);
   FP_LAUNCH_CHECK();
