@@ -263,8 +263,8 @@ __device__ __forceinline__ int lane_of_natural(int nt) { return 16 * (nt & 3) + 
 struct RecRef {
   uint32_t lo, hi;
   int vlen;  // bytes past the dense part; > kVarCap marks a raw record
-  __device__ __forceinline__ rsrc_t rs() const {
-    return make_rsrc(reinterpret_cast<const uint8_t*>((uint64_t)lo | ((uint64_t)hi << 32)), kRawRecord);
+  __device__ __forceinline__ rsrc_t rs(int bytes = kRawRecord) const {
+    return make_rsrc(reinterpret_cast<const uint8_t*>((uint64_t)lo | ((uint64_t)hi << 32)), bytes);
   }
 };
 
@@ -305,17 +305,25 @@ __device__ __forceinline__ RecRef page_ref(const PageMeta& m, int i, int kv) {
                             __builtin_amdgcn_readlane(m.vlen, l));
 }
 
+// Prefetches are issued on every path through the page loop, the same
+// instructions whether a record is coded or raw, present or not (``live``
+// false: the loads run against an empty range, return zeros and move no
+// data).  The compiler's wait before a decode then names exactly the loads
+// of the slab it reads; with a path that issues fewer loads it would also
+// wait on the prefetches issued after that slab (up to a memory round trip
+// per page).
+
 // Dense words of the wave's slab ``slab`` of record ``r``.
-__device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt, SlabBuf& b) {
-  load_slab(r.rs(), r.vlen > kVarCap, slab, nt, b);
+__device__ __forceinline__ void prefetch_dense(const RecRef& r, int slab, int nt, SlabBuf& b, bool live = true) {
+  load_slab(r.rs(live ? kRawRecord : 0), live && r.vlen > kVarCap, slab, nt, b);
 }
 
-// This lane's 8 bytes (at 512 w + 8 lane) of the record's variable region.
-// A wave whose quarter lies past the region (or a raw record) loads nothing.
+// This lane's 8 bytes (at 512 w + 8 lane) of the record's variable region;
+// zeros for a wave whose quarter lies past the region (or a raw record).
 __device__ __forceinline__ bool quarter_used(const RecRef& r, int w) { return r.vlen <= kVarCap && 512 * w < r.vlen; }
 
-__device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane) {
-  return quarter_used(r, w) ? rld8(r.rs(), 8 * lane, kDenseBytes + 512 * w) : make_uint2(0u, 0u);
+__device__ __forceinline__ uint2 prefetch_var(const RecRef& r, int w, int lane, bool live = true) {
+  return rld8(r.rs(live && quarter_used(r, w) ? kRawRecord : 0), 8 * lane, kDenseBytes + 512 * w);
 }
 
 // Per-record escape staging, done by all four waves from their prefetched
@@ -717,16 +725,17 @@ attn_kernel(AttnParams p) {
     __syncthreads();
     patch_raw(kr, vk, w, lane, sh.esc[0][0], sh.hdr[0][0]);
     patch_raw(vr, vv, w, lane, sh.esc[0][1], sh.hdr[0][1]);
-    if (second) {
-      vk = prefetch_var(nkr, w, lane);
-      vv = prefetch_var(nvr, w, lane);
-    }
+    vk = prefetch_var(nkr, w, lane, second);
+    vv = prefetch_var(nvr, w, lane, second);
 
     // a half takes pages half, half + 2, ...; both halves run the same
     // number of steps (and barriers): a step past a half's pages repeats its
     // last page with every key masked
     const int nsteps = kHalves == 2 ? (npages + 1) >> 1 : npages;
     for (int j = 0; j < nsteps; ++j) {
+      // (three workgroups share a CU at config 4's shape: the first
+      // dispatched finished its units ~30% before the last; rotated: even)
+      rotate_priority(j + blockIdx.x + blockIdx.y * gridDim.x);
       const int i = kHalves == 2 ? min(2 * j + half, npages - 1) : j;  // page of the unit
       const bool act = kHalves == 1 || 2 * j + half < npages;
       const int seq_m = act ? seq : 0;  // context this step's keys are masked against
@@ -734,19 +743,21 @@ attn_kernel(AttnParams p) {
       const bool more = act && i + kHalves < npages, more2 = act && i + 2 * kHalves < npages;
       const int tok0 = (p0 + i) * kTokens;
       // the page after next starts a new window of 64 block ids
-      if (more2 && ((i + 2 * kHalves) & 63) < kHalves)
+      if (more2 && ((i + 2 * kHalves) & 63) < kHalves) {
         meta = load_meta(p, load_block(bt, (i + 2 * kHalves) & ~63, npages, lane), h);
+        // read below: waited for here, so that no wait for it reaches the
+        // common path (where it would also wait on this page's K slab)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      }
       // V slab of this page in flight while K is decoded; the variable
       // regions of the page after next in flight for a whole page
       prefetch_dense(vr, w, nt, fv);
       RecRef nnkr = nkr, nnvr = nvr;
-      uint2 vk2 = make_uint2(0u, 0u), vv2 = make_uint2(0u, 0u);
       if (more2) {
         nnkr = page_ref(meta, i + 2 * kHalves, 0);
         nnvr = page_ref(meta, i + 2 * kHalves, 1);
-        vk2 = prefetch_var(nnkr, w, lane);
-        vv2 = prefetch_var(nnvr, w, lane);
       }
+      const uint2 vk2 = prefetch_var(nnkr, w, lane, more2), vv2 = prefetch_var(nnvr, w, lane, more2);
       __syncthreads();  // B1: this page's escapes patched; the previous page's V pass done everywhere
 
       // ---- S^T = K Q^T for tokens 32w .. 32w + 31 ----
@@ -807,8 +818,8 @@ attn_kernel(AttnParams p) {
         }
       };
       if (spec) softmax_tile(m_run);
+      prefetch_dense(nkr, w, nt, fk, more);
       if (more) {
-        prefetch_dense(nkr, w, nt, fk);
         expand_var(nkr, vk, w, lane, klut.s, sh.esc[par ^ 1][0], sh.hdr[par ^ 1][0]);
         expand_var(nvr, vv, w, lane, vlut.s, sh.esc[par ^ 1][1], sh.hdr[par ^ 1][1]);
       }

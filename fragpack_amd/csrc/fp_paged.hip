@@ -241,6 +241,7 @@ paged_decode_kernel(PagedParams p) {
     bool in_a = load_page<kPolicy>(p, bt[pg0], h, w, valid_of(pg0), lane, ka, stage0[w]), in_b = false;
     // two pages per trip so that each stage and fragment set is named statically
     for (int pg = pg0; pg < pg1; pg += 2) {
+      rotate_priority((pg >> 1) + blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
       if (pg + 1 < pg1) in_b = load_page<kPolicy>(p, bt[pg + 1], h, w, valid_of(pg + 1), lane, kb, stage1[w]);
       // page pg landed: only the next page's 16 transfers may still be in flight
       if (pg + 1 < pg1)

@@ -142,12 +142,30 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Sets this wave's instruction-issue priority to ``step`` mod 4 (wave-uniform).
+// The workgroups resident on one CU issue in age order when their priorities
+// are equal, so in a long-running launch the first-dispatched workgroup runs
+// ahead and the CU spends the end of the launch with fewer workgroups than it
+// can hold; kernels whose workgroups do equal work rotate the priority with
+// their loop step (offset by the workgroup id) to even out their progress.
+__device__ __forceinline__ void rotate_priority(int step) {
+  switch (step & 3) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Dense data of one kernel-order thread, as a lane holds it before decoding:
 //   coded: v[0..3] = low-byte chunks 0..3, v[4] = symbol words 0..3,
 //          v[5].x/y = symbol words 4..5;
 //   raw:   v[st] = word st (8 BF16 scalars) for st < 6; words 6 and 7 are
 //          read when decoded (raw records are rare: tails and fallbacks).
+// Both forms are loaded by the same instructions (four 16-byte loads, four
+// 8-byte loads) at offsets chosen by the form, so a caller's wait counts do
+// not depend on it.
 struct SlabBuf {
   uint4 v[6];
 };
@@ -240,33 +258,31 @@ __device__ __forceinline__ float2 ld_coh2(rsrc_t r, int64_t i) {
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Loads dense data of kernel-order thread 64 * slab + nt (nt < 64) of the
-// record behind ``r``.
+// record behind ``r`` (``raw`` wave-uniform): no branch, eight loads.
 __device__ __forceinline__ void load_slab(rsrc_t r, bool raw, int slab, int nt, SlabBuf& b) {
-  const int v16 = 16 * nt, v8 = 8 * nt;
-  if (raw) {
+  const int v16 = 16 * nt;
 #pragma unroll
-    for (int st = 0; st < 6; ++st) b.v[st] = rld16(r, v16, 4096 * st + 1024 * slab);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b.v[j] = rld16(r, v16, 4096 * j + 1024 * slab);
-    const uint2 s0 = rld8(r, v8, kLowBytes + 512 * slab);
-    const uint2 s1 = rld8(r, v8, kLowBytes + 2048 + 512 * slab);
-    const uint2 s2 = rld8(r, v8, kLowBytes + 4096 + 512 * slab);
-    b.v[4] = make_uint4(s0.x, s0.y, s1.x, s1.y);
-    b.v[5] = make_uint4(s2.x, s2.y, 0u, 0u);
-  }
+  for (int j = 0; j < 4; ++j) b.v[j] = rld16(r, v16, 4096 * j + 1024 * slab);
+  // symbol chunks m = 0..2 at 8 (256 m + t) and, past the record (zeros, no
+  // memory access), a fourth piece; or words 4 and 5 in 8-byte halves
+  const int vo = raw ? v16 : 8 * nt;
+  const uint2 s0 = rld8(r, vo, raw ? 4096 * 4 + 1024 * slab : kLowBytes + 512 * slab);
+  const uint2 s1 = rld8(r, vo, raw ? 4096 * 4 + 1024 * slab + 8 : kLowBytes + 2048 + 512 * slab);
+  const uint2 s2 = rld8(r, vo, raw ? 4096 * 5 + 1024 * slab : kLowBytes + 4096 + 512 * slab);
+  const uint2 s3 = rld8(r, vo, raw ? 4096 * 5 + 1024 * slab + 8 : kRawRecord);
+  b.v[4] = make_uint4(s0.x, s0.y, s1.x, s1.y);
+  b.v[5] = make_uint4(s2.x, s2.y, s3.x, s3.y);
 }
 
 // Loads thread ``t``'s (0..255) dense data of a record.
 __device__ __forceinline__ void load_thread(const uint8_t* rec, bool raw, int t, SlabBuf& b) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b.v[j] = ld16_nt(rec + 16 * (256 * j + t));
   if (raw) {
-#pragma unroll
-    for (int st = 0; st < 6; ++st) b.v[st] = ld16_nt(rec + 16 * (256 * st + t));
+    b.v[4] = ld16_nt(rec + 16 * (256 * 4 + t));
+    b.v[5] = ld16_nt(rec + 16 * (256 * 5 + t));
   } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b.v[j] = ld16_nt(rec + 16 * (256 * j + t));
-    const uint2 s0 = ld8_nt(rec + kLowBytes + 8 * t);
-    const uint2 s1 = ld8_nt(rec + kLowBytes + 8 * (256 + t));
+    const uint2 s0 = ld8_nt(rec + kLowBytes + 8 * t), s1 = ld8_nt(rec + kLowBytes + 8 * (256 + t));
     const uint2 s2 = ld8_nt(rec + kLowBytes + 8 * (512 + t));
     b.v[4] = make_uint4(s0.x, s0.y, s1.x, s1.y);
     b.v[5] = make_uint4(s2.x, s2.y, 0u, 0u);
@@ -427,23 +443,23 @@ __device__ __forceinline__ int thread_escapes(const SlabBuf& b) {
   return n;
 }
 
-// Raw-record data is already the BF16 words.
-// Raw-record data is already the BF16 words; words 6, 7 of thread ``t`` are
-// read here.
+// Raw-record data is already the BF16 words: words 0..5 come from the
+// SlabBuf, words 6 and 7 are read here.
 template <typename Emit>
-__device__ __forceinline__ void raw_words(const SlabBuf& b, const uint8_t* rec, int t, Emit&& emit) {
-  const uint4 w6 = ld16_nt(rec + 16 * (256 * 6 + t)), w7 = ld16_nt(rec + 16 * (256 * 7 + t));
+__device__ __forceinline__ void raw_tail(const SlabBuf& b, uint4 w6, uint4 w7, Emit&& emit) {
   static_for<0, 6>([&](auto st) { emit(st, b.v[st]); });
   emit(std::integral_constant<int, 6>{}, w6);
   emit(std::integral_constant<int, 7>{}, w7);
 }
 
 template <typename Emit>
+__device__ __forceinline__ void raw_words(const SlabBuf& b, const uint8_t* rec, int t, Emit&& emit) {
+  raw_tail(b, ld16_nt(rec + 16 * (256 * 6 + t)), ld16_nt(rec + 16 * (256 * 7 + t)), emit);
+}
+
+template <typename Emit>
 __device__ __forceinline__ void raw_words(const SlabBuf& b, rsrc_t r, int slab, int nt, Emit&& emit) {
-  const uint4 w6 = rld16(r, 16 * nt, 4096 * 6 + 1024 * slab), w7 = rld16(r, 16 * nt, 4096 * 7 + 1024 * slab);
-  static_for<0, 6>([&](auto st) { emit(st, b.v[st]); });
-  emit(std::integral_constant<int, 6>{}, w6);
-  emit(std::integral_constant<int, 7>{}, w7);
+  raw_tail(b, rld16(r, 16 * nt, 4096 * 6 + 1024 * slab), rld16(r, 16 * nt, 4096 * 7 + 1024 * slab), emit);
 }
 
 // Butterfly partner values across 16- and 32-lane halves with the gfx950
