@@ -728,14 +728,19 @@ attn_kernel(AttnParams p) {
     vk = prefetch_var(nkr, w, lane, second);
     vv = prefetch_var(nvr, w, lane, second);
 
+    // Workgroups L, L + cus, L + 2 cus (linear id L, cus = slots / kAttnPerCu)
+    // share a CU, dispatched in that order; at equal issue priority the
+    // oldest runs ahead (measured at config 4's shape: the three finished
+    // their units ~30% apart, the CU idling at the end).  Each page step sets
+    // the priority to (step + age rank) mod 4: at any step the three hold
+    // different priorities, rotating.
+    const int age = kHalves == 1 ? (int)(blockIdx.y * gridDim.x + blockIdx.x) / max(1, p.slots / kAttnPerCu) : 0;
     // a half takes pages half, half + 2, ...; both halves run the same
     // number of steps (and barriers): a step past a half's pages repeats its
     // last page with every key masked
     const int nsteps = kHalves == 2 ? (npages + 1) >> 1 : npages;
     for (int j = 0; j < nsteps; ++j) {
-      // (three workgroups share a CU at config 4's shape: the first
-      // dispatched finished its units ~30% before the last; rotated: even)
-      rotate_priority(j + blockIdx.x + blockIdx.y * gridDim.x);
+      rotate_priority(j + age);
       const int i = kHalves == 2 ? min(2 * j + half, npages - 1) : j;  // page of the unit
       const bool act = kHalves == 1 || 2 * j + half < npages;
       const int seq_m = act ? seq : 0;  // context this step's keys are masked against
@@ -973,19 +978,6 @@ attn_kernel(AttnParams p) {
 }  // namespace fp
 
 using namespace fp;
-
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev] = cus;
-  }
-  return cache[dev];
-}
 
 
 namespace fp {

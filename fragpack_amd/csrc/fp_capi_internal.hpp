@@ -8,6 +8,19 @@
 
 namespace fp {
 void set_error(const char* msg);
+
+// Compute units of the current device (cached per device; 0 if unknown).
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
 }  // namespace fp
 
 #define FP_CHECK(cond, msg)   \

@@ -71,6 +71,7 @@ struct PagedParams {
   int64_t q_stride, out_stride, bt_stride;
   int64_t num_blocks;  // pages in the caches: block ids outside [0, num_blocks) are skipped
   int kvh, group, splits, ppc;
+  int cus;  // compute units of the device
   float scale_log2;
 };
 
@@ -236,12 +237,16 @@ paged_decode_kernel(PagedParams p) {
   for (int dt = 0; dt < 8; ++dt) st.o[dt] = pg_f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (pg0 < pg1) {
+    // workgroups L and L + cus (linear id L) share a CU, the older issuing
+    // first at equal priority: the priority rotates with the page pair,
+    // offset by the dispatch round, so the two progress evenly
+    const int age = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) / max(1, p.cus);
     KFrag ka, kb;
     auto valid_of = [&](int pg) { return min(128, len - pg * 128); };
     bool in_a = load_page<kPolicy>(p, bt[pg0], h, w, valid_of(pg0), lane, ka, stage0[w]), in_b = false;
     // two pages per trip so that each stage and fragment set is named statically
     for (int pg = pg0; pg < pg1; pg += 2) {
-      rotate_priority((pg >> 1) + blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+      rotate_priority((pg >> 1) + age);
       if (pg + 1 < pg1) in_b = load_page<kPolicy>(p, bt[pg + 1], h, w, valid_of(pg + 1), lane, kb, stage1[w]);
       // page pg landed: only the next page's 16 transfers may still be in flight
       if (pg + 1 < pg1)
@@ -434,6 +439,7 @@ extern "C" int fp_paged_decode(const void* q, int64_t q_stride, int64_t batch, i
   p.splits = (int)splits;
   p.ppc = (int)((pages + splits - 1) / splits);
   p.scale_log2 = (float)(scale * 1.4426950408889634);
+  p.cus = device_cus();
   const dim3 grid((unsigned)splits, (unsigned)kv_heads, (unsigned)batch);
   if (g_paged_streaming)
     hipLaunchKernelGGL(paged_decode_kernel<kNt>, grid, dim3(kPgThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
