@@ -397,6 +397,11 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
   // literal operand would cost a separate v_xor)
   uint32_t c0c;
   asm("s_mov_b32 %0, 0x0c0c0c0c" : "=s"(c0c));
+  // the running escape position as an LDS byte address (``esc`` is 4-byte
+  // aligned, so its low two bits are those of eo)
+  typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+  typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+  uint32_t ea = (uint32_t)(uintptr_t)(lds_u8*)esc + (uint32_t)eo;
   static_for<0, 8>([&](auto st_c) {
     constexpr int st = decltype(st_c)::value;
     const uint32_t sk = sym_word(b, st);
@@ -405,12 +410,11 @@ __device__ __forceinline__ void decode_words(const SlabBuf& b, const uint8_t* es
     // primary high bytes of scalars 0,2,4,6 / 1,3,5,7 (escape code 7 -> 0)
     const uint32_t hp_ev = perm(lut1, lut0, s_ev);
     const uint32_t hp_od = perm(lut1, lut0, s_od);
-    const int a = eo & ~3;
-    const uint32_t* ew = reinterpret_cast<const uint32_t*>(esc + a);
+    lds_u32* ew = (lds_u32*)(uintptr_t)(ea & ~3u);
     const uint32_t d0 = ew[0], d1 = ew[1], d2 = ew[2];
-    // v_alignbyte_b32 shifts by 8 x bits [1:0] of its last operand: eo as is
-    const uint2 win = make_uint2(alignbyte(d1, d0, (uint32_t)eo), alignbyte(d2, d1, (uint32_t)eo));
-    eo += __builtin_popcount(b8);
+    // v_alignbyte_b32 shifts by 8 x bits [1:0] of its last operand: ea as is
+    const uint2 win = make_uint2(alignbyte(d1, d0, ea), alignbyte(d2, d1, ea));
+    ea += __builtin_popcount(b8);
     // nibble i of rank: escapes among nibbles < i (b8 = 8 x the escape bits)
     const uint32_t rank = b8 * 0x02222222u;
     // selector byte per scalar: its rank for an escape, 0x0C (-> byte 0x00)
