@@ -311,10 +311,13 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
           s[2][qt] = pf_mfma(k2, qf[qt][ks], s[2][qt]);
           s[3][qt] = pf_mfma(k3, qf[qt][ks], s[3][qt]);
         }
-        // (kt, qt) pairs ks * kPfQt / 2 .. of keys 0..31: kt = pair / kPfQt
+        // (kt, qt) pairs ks * kPerStep .. of keys 0..31 (2 kPfQt pairs over
+        // the four k-steps): kt = pair / kPfQt
+        constexpr int kPerStep = (2 * kPfQt + 3) / 4;
 #pragma unroll
-        for (int u = 0; u < kPfQt / 2; ++u) {
-          const int pr = ks * (kPfQt / 2) + u, kt = pr / kPfQt, qt = pr % kPfQt;
+        for (int u = 0; u < kPerStep; ++u) {
+          const int pr = ks * kPerStep + u, kt = pr / kPfQt, qt = pr % kPfQt;
+          if (pr >= 2 * kPfQt) continue;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             e[kt][qt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][qt][r], p.scale_log2, nm[qt]));
