@@ -97,6 +97,10 @@ int fp_fused_decode(const void* q, int64_t q_stride, int64_t batch, int64_t kv_h
  * the sequence's last (seq_lens[b] - 1), in its last block.
  *   new_k, new_v  BF16 [B, H, 128]: token / head strides in elements (even)
  *   slot_mapping  int64 [B]
+ * Currently disabled: the call records an error (fp_last_error) and returns
+ * -1 without launching anything, because its first GPU run faulted and the
+ * cause has not been shown.  Callers write with fp_hbm_write (or the fused
+ * fp_hbm_write_encode) and then call fp_fused_decode.
  */
 int fp_fused_decode_append(const void* q, int64_t q_stride, int64_t batch, int64_t kv_heads, int64_t group,
                            const int64_t* rec_addr, const int32_t* rec_len, const uint32_t* plut,
