@@ -471,9 +471,9 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane) {
+__device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane, int len) {
   InlinePlan r;
-  r.len = lane < p.batch ? p.seq_lens[lane] : 0;
+  r.len = len;
   r.n = (r.len + 127) >> 7;
   const int longest = wave_total<true>(r.n);
   const int cand = max(1, (longest + lane) / (lane + 1));
@@ -594,11 +594,29 @@ attn_kernel(AttnParams p) {
   __shared__ int plan_s[kInlinePlan ? kWaves * kHalves : 1][4][64];
   int(&wplan)[4][64] = plan_s[kInlinePlan ? wave : 0];  // this wave's rows
   const bool bt_lds = kInlinePlan && p.bt_lds;
-  if (bt_lds)
-    for (int i = threadIdx.x; i < p.batch * (int)p.bt_stride; i += 64 * kWaves * kHalves) bt_s[i] = p.block_table[i];
-  if constexpr (kInlinePlan) ip = inline_plan(p, lane);
+  // A planning launch's first global hop carries the sequence lengths and the
+  // block table together (the table's LDS stores wait only for its own loads).
+  const int len0 = kInlinePlan && lane < p.batch ? p.seq_lens[lane] : 0;
+  if (bt_lds) {
+    constexpr int kStride = 64 * kWaves * kHalves;
+    int v[(kBtLds + kStride - 1) / kStride];
+#pragma unroll
+    for (int k = 0; k < (kBtLds + kStride - 1) / kStride; ++k) {
+      const int i = threadIdx.x + k * kStride;
+      v[k] = i < p.batch * (int)p.bt_stride ? p.block_table[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < (kBtLds + kStride - 1) / kStride; ++k) {
+      const int i = threadIdx.x + k * kStride;
+      if (i < p.batch * (int)p.bt_stride) bt_s[i] = v[k];
+    }
+  }
+  if constexpr (kInlinePlan) ip = inline_plan(p, lane, len0);
   if (bt_lds) __syncthreads();
-  const int used = kInlinePlan ? ip.used : uniform(p.plan[1]);  // units in use
+  // units in use; a launch reusing the plan walks its units until the first
+  // idle one instead (every planner marks units [used, units) idle), so its
+  // first hop is the unit descriptor itself, not the plan's unit count
+  const int used = kInlinePlan ? ip.used : p.units;
   const int ppc = ip.ppc;
   if constexpr (kInlinePlan) {
     // the per-sequence plan goes to this wave's LDS rows (read back by
@@ -642,7 +660,7 @@ attn_kernel(AttnParams p) {
       const int4 u0 = udp[0], u1 = udp[1];
       asm volatile("" ::"v"(u0.x), "v"(u0.y), "v"(u0.z), "v"(u0.w), "v"(u1.x), "v"(u1.y), "v"(u1.z), "v"(u1.w));  // one hop
       b = uniform(u0.x);
-      if (b < 0) continue;
+      if (b < 0) break;  // idle: so are this workgroup's later units
       p0 = uniform(u0.y);
       npages = uniform(u0.z);
       seq = uniform(u0.w);
