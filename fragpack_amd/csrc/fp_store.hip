@@ -33,6 +33,10 @@ enum : int {
   kSpills = 8,
   kHeirs = 9,
   kDonors = 10,
+  // this build's: the claim-mode encode's dynamic tail (record cursor and
+  // finished workgroups), both zero between launches
+  kEncCursor = 11,
+  kEncDone = 12,
 };
 // tags rows: [0] prepare's list of late closing claims (<= NB entries), [1..3] per-block step stamps
 enum : int { kLateList = 0, kTagClose = 1, kTagClaim = 2, kTagCloseDedupe = 3 };
@@ -667,6 +671,7 @@ struct EncShared {
   uint32_t var32[kVarCap / 4];
   int wsum[2][8];  // per 32-thread slab: escapes, raws
   int s_off, s_ovf;
+  int dyn_start;  // claim-mode tail: the start of the batch thread 0 grabbed last
 };
 
 // LDS table entry of rank r (the store's rank_of byte: 0..21, 255 absent).
@@ -921,12 +926,30 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   }
   int r = kBlockMajor ? (int)blockIdx.x * per : (int)blockIdx.x;
   if (r >= n_rec) return;
+  // Claim-mode encode: each workgroup takes records x, x + grid, ... for the
+  // first 7/8 of the rounds; the rest go out kDynBatch consecutive records at
+  // a time from a cursor in the counters, so that workgroups that run faster
+  // (the first dispatched on each CU; some XCDs) take more of them and the
+  // launch ends when the average workgroup does (measured on MI355X with
+  // static rounds only: workgroups ended within 4.9-5.7 ms of a 5.7 ms
+  // launch).  A batch is grabbed one batch ahead (thread 0; published
+  // through LDS at the end of the iteration) and its records' metadata
+  // loaded when it is published.  The last workgroup to finish resets both
+  // counters.
+  constexpr bool kDyn = kMode == kEncClaim;
+  constexpr int kDynBatch = 4;
   // Record metadata (block, heir, staging slot) of this workgroup's records
   // in batches of 64 (record r + j grid in lane j), loaded with vector loads
   // one batch ahead: scalar loads would be waited for at every LDS barrier.
   // The stage streams record r + grid while r is encoded.
   const int g = kWrite ? tk.enc_grid : (int)gridDim.x;
   const int lane = tid & 63;
+  // (with fewer than 8 rounds the launch stays static: every workgroup then
+  // has records, so every one reaches the counter that ends the tail)
+  const int rounds = n_rec / g;
+  const bool dyn = kDyn && rounds >= 8;
+  const int k_static = dyn ? rounds - rounds / 8 : (1 << 30);
+  const int n_static = dyn ? k_static * g : n_rec;
   // the k-th record of this workgroup: its block (close index) and (kv, head)
   auto rec_kvh = [&](int rr) { return kBlockMajor ? rr % per : rr / n_closes; };
   auto next_rec = [&](int rr) { return kBlockMajor ? (rr % per == per - 1 ? rr + 1 + (g - 1) * per : rr + 1) : rr + g; };
@@ -946,6 +969,22 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   int cb, ch, cw, nb, nh, nw;  // current / next batch
   load_meta(0, cb, ch, cw);
   load_meta(64, nb, nh, nw);
+  // dynamic tail: the current batch [dyn_end - kDynBatch, dyn_end) and the
+  // next one (start dyn_next, metadata of its record j in lane j of dn*)
+  int dyn_end = 0, dyn_next = 0, dmb = 0, dmh = -1, dmw = 0, dnb = 0, dnh = -1, dnw = 0;
+  int grabbed = 0;  // thread 0: the batch start to publish at the end of the iteration
+  auto load_dyn_meta = [&](int start, int& mb, int& mh, int& mw) {
+    mb = 0;
+    mh = -1;
+    mw = 0;
+    const int rr = start + lane;
+    if (lane < kDynBatch && rr < n_rec) {
+      const int ci = rr % n_closes;
+      mb = s.close_list[ci];
+      mh = s.close_list[s.cap + ci];
+      mw = s.wslot[mb];
+    }
+  };
   int b = __builtin_amdgcn_readfirstlane(cb);
   int heir = __builtin_amdgcn_readfirstlane(ch);
   uint8_t* src = staging_addr(s, __builtin_amdgcn_readfirstlane(cw), layer, rec_kvh(r));
@@ -957,7 +996,8 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
   int n_enc = 0, n_fall = 0, n_err = 0, n_spill = 0;
   bool ovf_full = false;  // this workgroup found the overflow pool full
   int boff = 0;           // ordered encode: the block's next free page byte (thread 0)
-  for (int k = 0; r < n_rec; r = next_rec(r), ++k) {
+  int r_next = r;
+  for (int k = 0; r < n_rec; r = r_next, ++k) {
     const int kvh = rec_kvh(r);
     const int64_t idx = ((int64_t)layer * s.NB + b) * per + kvh;
     int32_t* fill = s.fill + (int64_t)layer * s.NB + b;
@@ -987,11 +1027,38 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
     // the next record's metadata: lane (k + 1) % 64 of the current or next batch
     const int k1 = (k + 1) & 63;
     const bool nbatch = k1 == 0;
-    const int b1 = __builtin_amdgcn_readlane(nbatch ? nb : cb, k1);
-    const int heir1 = __builtin_amdgcn_readlane(nbatch ? nh : ch, k1);
-    const int w1 = __builtin_amdgcn_readlane(nbatch ? nw : cw, k1);
+    int b1 = __builtin_amdgcn_readlane(nbatch ? nb : cb, k1);
+    int heir1 = __builtin_amdgcn_readlane(nbatch ? nh : ch, k1);
+    int w1 = __builtin_amdgcn_readlane(nbatch ? nw : cw, k1);
     uint8_t* src1 = src;
-    const int r1 = next_rec(r);
+    int r1 = next_rec(r);
+    bool new_batch = false;
+    if (dyn && k + 1 >= k_static) {
+      if (r + 1 < dyn_end) {  // the current tail batch goes on
+        r1 = r + 1;
+        const int j = r1 - (dyn_end - kDynBatch);
+        b1 = __builtin_amdgcn_readlane(dmb, j);
+        heir1 = __builtin_amdgcn_readlane(dmh, j);
+        w1 = __builtin_amdgcn_readlane(dmw, j);
+      } else {  // the next batch: grabbed one batch ago, metadata loaded
+        r1 = dyn_next;
+        dyn_end = dyn_next + kDynBatch;
+        dmb = dnb;
+        dmh = dnh;
+        dmw = dnw;
+        b1 = __builtin_amdgcn_readlane(dmb, 0);
+        heir1 = __builtin_amdgcn_readlane(dmh, 0);
+        w1 = __builtin_amdgcn_readlane(dmw, 0);
+        new_batch = r1 < n_rec;
+      }
+      r1 = min(r1, n_rec);
+    }
+    // the first tail batch is grabbed three records before the static rounds
+    // end (workgroups get there at different times, so the grabs spread out),
+    // each later one when the batch before it starts
+    if (dyn && k == k_static - 3) new_batch = true;
+    if (new_batch && tid == 0) grabbed = n_static + atomicAdd(&s.counters[kEncCursor], kDynBatch);
+    r_next = r1;
     if (r1 < n_rec) {
       src1 = staging_addr(s, w1, layer, rec_kvh(r1));
       if constexpr (kWrite) write_own_rows(s, tk, layer, b1, heir1, rec_kvh(r1));
@@ -1115,10 +1182,22 @@ encode_kernel(Store s, int layer, uint8_t* arena, int64_t page_bytes, const uint
       }
     }
     if (kBlockMajor && tid == 0 && kvh == per - 1) *fill = boff;  // the block's records are placed
+    if (new_batch && tid == 0) sh.dyn_start = grabbed;
     lds_barrier();  // sh (var32, s_off, s_ovf; rank on a head change) is reused by the next record
+    if (new_batch) {
+      dyn_next = __builtin_amdgcn_readfirstlane(sh.dyn_start);
+      load_dyn_meta(dyn_next, dnb, dnh, dnw);
+    }
     b = b1;
     heir = heir1;
     src = src1;
+  }
+  if (dyn && tid == 0) {
+    // every workgroup has made its last grab: the last one out resets the tail
+    if (atomicAdd(&s.counters[kEncDone], 1) == g - 1) {
+      s.counters[kEncCursor] = 0;
+      s.counters[kEncDone] = 0;
+    }
   }
   if (tid == 0) {
     if (n_enc) atomicAdd(&s.counters[kEncoded], n_enc);

@@ -622,3 +622,54 @@ def test_random_serving_steps(fused):
     closed = sorted(b for b, n in eng.filled.items() if n == T)
     eng.check_records(closed)
     eng.check_gather()
+
+
+def test_encode_dynamic_tail_across_launches():
+    """A claim-mode encode of at least eight rounds per workgroup hands its
+    last records out from a cursor that the launch's last workgroup resets:
+    two layers of 1024 closed blocks (H 8: 16 rounds over MI355X's 1024
+    encode workgroups) encoded one launch after the other both place every
+    record (none left pointing at staging), the counts add up, both tail
+    counters read zero after each launch, and every record gathers back
+    bit for bit."""
+    import torch
+
+    from fragpack_amd.compression.attn_tables import device_tables
+    from fragpack_amd.ops import hbm_kv
+    from fragpack_amd.ops.hbm_kv import HbmKvStore, page_bytes
+    from tests import workloads
+
+    H, n, L = 8, 1024, 2
+    rng = np.random.default_rng(77)
+    scales = workloads.channel_scales(rng, H, 0.02)
+    tables = np.repeat(workloads.calibrated_tables(rng, H, scales), L, axis=0)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(77)
+    scales_t = torch.from_numpy(scales).float().to(dev)
+    arenas = [torch.empty((n, page_bytes(H)), dtype=torch.uint8, device=dev) for _ in range(L)]
+    store = HbmKvStore(arenas, H, device_tables(tables, dev), max_tokens=n * T, staging_slots=1,
+                       overflow_records=8192)
+    slots = torch.arange(n * T, device=dev, dtype=torch.int64)
+    store.prepare(slots, slots.numel(), np.zeros(0, np.int32))
+    # blocks closing in their own step hold transient slots of one layer's
+    # size: each layer is written and encoded in turn, as a forward does
+    held = [(t.data_ptr(), t.data_ptr() + t.numel()) for t in (store.staging, store.scratch)]
+    for layer in range(L):
+        kv = workloads.gen_kv(torch, gen, n * T, H, scales_t)
+        store.write(layer, kv[0], kv[1], slots)
+        store.encode(layer, n)
+        torch.cuda.synchronize()
+        c = store.counters.cpu().numpy()
+        print("layer", layer, "counters", c.tolist(), flush=True)
+        assert int(c[hbm_kv._ENCODED]) == (layer + 1) * n * 2 * H
+        assert int(c[11]) == 0 and int(c[12]) == 0, "the tail cursor is reset for the next launch"
+        addr = store.rec_addr[layer].cpu().numpy()
+        for lo, hi in held:
+            assert not np.any((addr >= lo) & (addr < hi)), "a record was left in staging"
+        blocks = torch.arange(n, dtype=torch.int32, device=dev)
+        wk = torch.empty((n, T, H, D), dtype=torch.bfloat16, device=dev)
+        wv = torch.empty_like(wk)
+        store.gather(layer, blocks, wk, wv)
+        ref = kv.view(2, n, T, H, D)
+        assert torch.equal(wk.view(torch.int16), ref[0].view(torch.int16))
+        assert torch.equal(wv.view(torch.int16), ref[1].view(torch.int16))
