@@ -84,6 +84,7 @@ struct AttnParams {
   int inline_plan;  // 1: every workgroup plans for itself (batch <= 64)
   int bt_lds;       // inline plan and the whole block table (batch x bt_stride <= kBtLds) read into LDS
   float scale_log2;
+  float lazy;  // kLazyMax / scale_log2: the softmax reference's headroom in score units
 };
 
 // Plan layout (int32): [0] ppc, [1] units in use, [2, 2 + 2 units) (sequence, first
@@ -120,10 +121,13 @@ constexpr int kPlanLds = 8192;
 constexpr int kPlanCands = 64;
 constexpr int kUnitCost = 1;  // fixed cost of a unit (metadata, Q, merge) in pages
 
-struct Divider {  // x / d for 0 <= x < 2^24, 1 <= d
+// x / d for 0 <= x < 2^22, 1 <= d.  inv is the hardware reciprocal (relative
+// error <= 2^-23), so x * inv is within 1.5 * 2^-23 * x / d < 0.75 of x / d:
+// its truncation is off by at most one, which div's two steps correct.
+struct Divider {
   int d;
   float inv;
-  __device__ explicit Divider(int d_) : d(d_), inv(1.0f / (float)d_) {}
+  __device__ explicit Divider(int d_) : d(d_), inv(__builtin_amdgcn_rcpf((float)d_)) {}
   __device__ __forceinline__ int div(int x) const {
     int q = (int)((float)x * inv);
     q += (q + 1) * d <= x;
@@ -476,13 +480,13 @@ __device__ __forceinline__ InlinePlan inline_plan(const AttnParams& p, int lane,
   r.len = len;
   r.n = (r.len + 127) >> 7;
   const int longest = wave_total<true>(r.n);
-  const int cand = max(1, (longest + lane) / (lane + 1));
+  const int cand = max(1, Divider(lane + 1).div(longest + lane));
   const Divider dv(cand);
   int chunks = 0;
   for (int b = 0; b < p.batch; ++b) chunks += dv.chunks(__builtin_amdgcn_readlane(r.n, b));
   uint64_t key = ~0ull;
   if (chunks <= p.units) {
-    // (chunks * kvh + slots < 2^24 for an inline-planning launch: Divider's range)
+    // (chunks * kvh + slots < 2^22 for an inline-planning launch: Divider's range)
     const int rounds = Divider(p.slots).div(chunks * p.kvh + p.slots - 1);
     key = ((uint64_t)(rounds * ((cand + p.halves - 1) >> (p.halves - 1)) + rounds * kUnitCost) << 24) |
           (uint64_t)(0xFFFFFF - cand);
@@ -569,7 +573,19 @@ __device__ __forceinline__ void merge_chunks(const AttnParams& p, AttnShared& sh
 // the whole 256-register budget)
 template <bool kInlinePlan, int kHalves>
 __global__ void __launch_bounds__(64 * kWaves * kHalves) __attribute__((amdgpu_waves_per_eu(kHalves == 2 ? 2 : kAttnPerCu)))
-attn_kernel(AttnParams p) {
+attn_kernel(AttnParams pk) {
+  // Two-half launches pass the scalar parameters through an empty asm once,
+  // at entry, so the compiler keeps them in SGPRs instead of reloading them
+  // from the kernel arguments (dependent scalar-load round trips) where they
+  // are used: in a planning launch those reloads sat between the plan and the
+  // first unit.  The pointers stay as they are (an asm operand would lose
+  // their address space and turn their loads into flat loads).  One-half
+  // launches skip it: the longer-lived SGPRs would spill VGPRs there.
+  AttnParams p = pk;
+  if constexpr (kHalves == 2) {
+    asm volatile("" : "+s"(p.q_stride), "+s"(p.out_stride), "+s"(p.bt_stride), "+s"(p.kvh), "+s"(p.group), "+s"(p.units),
+                 "+s"(p.batch), "+s"(p.ud_off), "+s"(p.slots), "+s"(p.halves), "+s"(p.bt_lds), "+s"(p.scale_log2), "+s"(p.lazy));
+  }
   __shared__ AttnShared shs[kHalves];
   const int lane = wave_lane();
   const int wave = uniform((int)(threadIdx.x >> 6));
@@ -728,7 +744,7 @@ attn_kernel(AttnParams p) {
       }
     }
     float m_run = -INFINITY, l_run = 0.f;  // m_run: unscaled score units
-    const float lazy = kLazyMax / p.scale_log2;
+    const float lazy = p.lazy;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
     expand_var(kr, vk, w, lane, klut.s, sh.esc[0][0], sh.hdr[0][0]);
     expand_var(vr, vv, w, lane, vlut.s, sh.esc[0][1], sh.hdr[0][1]);
@@ -1017,6 +1033,8 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   FP_CHECK(opart_elems >= kv_heads * units * 8 * kDim && ml_elems >= kv_heads * units * 16,
            "decode workspace too small");
   FP_CHECK(units < (1 << 24) && batch < (1 << 24), "batch too large");
+  // (page counts and their chunk arithmetic stay inside the planners' 2^22 range)
+  FP_CHECK(bt_stride >= 0 && bt_stride < (1 << 21), "block table rows must hold fewer than 2^21 pages");
   FP_CHECK(kv_heads * units * 8 * kDim * 4 < (1LL << 31), "decode workspace must stay below 2 GiB");
   FP_CHECK(plan_elems >= ud_offset((int)units) + 8 * units + units * kv_heads,
            "decode plan workspace too small (see workspace_elems)");
@@ -1041,6 +1059,7 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   p.ud_off = ud_offset((int)units);
   p.done = plan + plan_elems - units * kv_heads;
   p.scale_log2 = (float)(scale * 1.4426950408889634);
+  p.lazy = kLazyMax / p.scale_log2;
   const int cus = device_cus();
   FP_CHECK(cus > 0, "cannot query the device's compute-unit count");
   // resident workgroups: kAttnPerCu 4-wave ones per CU, or one two-half
@@ -1052,7 +1071,7 @@ int decode_launch(AttnParams& p, const void* q, int64_t q_stride, int64_t batch,
   // replan 2 / 3: plan inside the attention kernel (batch <= 64; the merge
   // counters must be as a previous completed call left them, i.e. zero)
   FP_CHECK(replan >= 0 && replan <= 3, "replan must be 0, 1, 2 or 3");
-  p.inline_plan = (replan == 2 || replan == 3) && batch <= 64 && units * kv_heads + slots < (1 << 24);
+  p.inline_plan = (replan == 2 || replan == 3) && batch <= 64 && units * kv_heads + slots < (1 << 22);
   p.bt_lds = replan == 3 && p.inline_plan && batch * bt_stride <= kBtLds;
   if (replan && !p.inline_plan) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, seq_lens, block_table, bt_stride, plan,
