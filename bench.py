@@ -896,6 +896,38 @@ def hbm_ceilings(torch) -> dict:
     return out
 
 
+def mix_ceiling(torch, enc) -> dict:
+    """The HBM rate of the encoder's own read / write mix with no computation:
+    the streaming probe over as many 32 KB records as config 3 encodes, each
+    read whole and ``written / records`` of it (rounded to 16 bytes) written
+    back, at the encoder's four workgroups per CU and at eight."""
+    from fragpack_amd.ops.fragpack_ext import extension
+
+    ext = extension()
+    n = enc["records"]
+    wb = int(round((enc["read_write_bytes"] - n * 32768) / n / 16)) * 16
+    src = torch.ones(n * 32768, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    out = {"records": n, "read_bytes": 32768, "write_bytes": wb}
+    for wg in (4, 8):
+        fn = lambda: ext.stream_probe(src, dst, 32768, wb, wg)  # noqa: E731
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 5
+        out[f"GBps_{wg}_per_cu"] = round(n * (32768 + wb) / ms / 1e6, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    log(f"encoder-mix ceiling: {out}")
+    return out
+
+
 def cpu_baseline(torch, res, args) -> dict:
     """The CPU oracle (C, OpenMP) on the same decode step: decode every record
     of the 4 x 8192-token layer and run fp32 attention, timed on this host's
@@ -1224,6 +1256,10 @@ def main() -> None:
             line["decode_large"]["frac_of_read_ceiling"] = round(la / ceil["read_GBps"], 4)
         if enc is not None:
             line["encode"]["frac_of_copy_ceiling"] = round(enc["read_write_bytes"] / enc["ms"] / 1e6 / ceil["copy_GBps"], 4)
+            mix = mix_ceiling(torch, enc)
+            line["encode"]["mix_ceiling"] = mix
+            line["encode"]["frac_of_mix_ceiling"] = round(
+                enc["read_write_bytes"] / enc["ms"] / 1e6 / max(mix["GBps_4_per_cu"], mix["GBps_8_per_cu"]), 4)
     print(json.dumps(line))
 
 

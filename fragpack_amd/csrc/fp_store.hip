@@ -1307,6 +1307,32 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const int32_t* src, co
   store_tile(sh, out, (int64_t)H * kTileRow);
 }
 
+// Streaming probe: record r (32 KB-strided in src and dst) reads its first
+// rb bytes and writes its first wb of them back to dst, records r =
+// blockIdx.x, + gridDim.x, ...; eight 16-byte non-temporal loads per thread
+// in flight, then the stores.  No computation: the HBM rate of a given
+// read / write mix at a given number of bytes in flight per CU, for reading
+// the encoder's rate against.
+__global__ void __launch_bounds__(kThreads) stream_probe_kernel(const uint8_t* src, uint8_t* dst, int64_t n, int rb,
+                                                               int wb) {
+  const int tid = threadIdx.x;
+  for (int64_t r = blockIdx.x; r < n; r += gridDim.x) {
+    const uint8_t* from = src + r * kRawRecord;
+    uint8_t* to = dst + r * kRawRecord;
+    uint4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int o = 16 * (tid + kThreads * k);
+      v[k] = o < rb ? ld16_nt(from + o) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int o = 16 * (tid + kThreads * k);
+      if (o < wb) st16_nt(to + o, v[k]);
+    }
+  }
+}
+
 // grid (n): record i (any table, K or V) -> out [i, 128, 128].
 __global__ void __launch_bounds__(kThreads) decode_records_kernel(const int64_t* rec_addr, const int32_t* rec_len,
                                                                  const int32_t* kv, const uint32_t* plut,
@@ -1808,6 +1834,25 @@ extern "C" int fp_hbm_gather(const int32_t* src_blocks, int64_t n, const int64_t
   hipLaunchKernelGGL(gather_kernel, dim3((unsigned)n, (unsigned)(2 * kv_heads)), dim3(kThreads), sizeof(DecShared),
                      stream, src_blocks, rec_addr, rec_len, plut, slut, static_cast<uint8_t*>(wk),
                      static_cast<uint8_t*>(wv), (int)kv_heads);
+  FP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int fp_stream_probe(const void* src, void* dst, int64_t records, int64_t read_bytes, int64_t write_bytes,
+                               int64_t wg_per_cu, fp_stream_t stream) {
+  if (records == 0) return 0;
+  FP_CHECK(records > 0 && wg_per_cu > 0 && wg_per_cu <= 8, "bad probe geometry");
+  FP_CHECK(read_bytes >= 0 && read_bytes <= kRawRecord && read_bytes % 16 == 0 && write_bytes >= 0 &&
+               write_bytes <= read_bytes && write_bytes % 16 == 0,
+           "probe bytes must be multiples of 16 with write <= read <= 32768");
+  FP_CHECK(reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0,
+           "probe buffers must be 16-byte aligned");
+  const int cus = device_cus();
+  FP_CHECK(cus > 0, "cannot query the device's compute-unit count");
+  const int64_t grid = std::min<int64_t>(records, wg_per_cu * cus);
+  hipLaunchKernelGGL(stream_probe_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), records, (int)read_bytes,
+                     (int)write_bytes);
   FP_LAUNCH_CHECK();
   return 0;
 }

@@ -118,6 +118,7 @@ class Extension:
                                     _i32, _p],
             "fp_hbm_commit": [sp, _p],
             "fp_hbm_gather": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _p],
+            "fp_stream_probe": [_p, _p, _i64, _i64, _i64, _i64, _p],
             "fp_hbm_export": [_p, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p],
             "fp_hbm_import": [sp, _p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p],
             "fp_encode_records": [_p, _i64, _p, _p, _p, _i64, _p, _p, _p],
@@ -271,6 +272,15 @@ class Extension:
         self._call("fp_hbm_gather", _dev(src_blocks, "src_blocks"), n, _dev(rec_addr, "rec_addr"),
                    _dev(rec_len, "rec_len"), _dev(plut, "plut"), _dev(slut, "slut"), _dev(wk, "wk"),
                    _dev(wv, "wv"), ws, int(kv_heads), _stream(wk))
+
+    def stream_probe(self, src, dst, read_bytes: int, write_bytes: int, wg_per_cu: int) -> None:
+        """Streaming probe (measurement only): per 32 KB record of ``src``
+        read ``read_bytes`` and write the first ``write_bytes`` of them to
+        ``dst``."""
+        _check(src.dtype == torch.uint8 and dst.dtype == torch.uint8 and src.is_contiguous() and dst.is_contiguous()
+               and src.numel() == dst.numel() and src.numel() % 32768 == 0, "probe buffers: equal uint8 [n * 32768]")
+        self._call("fp_stream_probe", _dev(src, "src"), _dev(dst, "dst"), src.numel() // 32768, int(read_bytes),
+                   int(write_bytes), int(wg_per_cu), _stream(src))
 
     def hbm_export(self, blocks, rec_addr, rec_len, out, stride: int, lengths, digest: int) -> None:
         n = blocks.numel()

@@ -205,6 +205,15 @@ int fp_hbm_write_encode(const fp_store_t* s, const void* key, int64_t k_s0, int6
  * (fragpack_ext.cpp:35-39, hbm_kv.cu:725-734). */
 int fp_hbm_commit(const fp_store_t* s, fp_stream_t stream);
 
+/* Streaming probe, no counterpart in the reference: for r < records, reads
+ * the first read_bytes of src + 32768 r and writes the first write_bytes of
+ * them to dst + 32768 r (non-temporal, wg_per_cu 256-thread workgroups per
+ * CU, each with 32 KB of loads in flight).  bench.py times it as the HBM
+ * ceiling for the encoder's read / write mix.  Buffers: records x 32768
+ * bytes each, 16-byte aligned; bytes multiples of 16, write <= read <= 32768. */
+int fp_stream_probe(const void* src, void* dst, int64_t records, int64_t read_bytes, int64_t write_bytes,
+                    int64_t wg_per_cu, fp_stream_t stream);
+
 /* Decode records of blocks src_blocks[i] (one layer's rec tables, [NB, 2, H])
  * into token-major BF16 pages wk / wv [>= n, 128, H, 128] (ws_bytes each).
  * Replaces hbm_gather (fragpack_ext.cpp:41-43, hbm_kv.cu:736-753). */

@@ -673,3 +673,25 @@ def test_encode_dynamic_tail_across_launches():
         ref = kv.view(2, n, T, H, D)
         assert torch.equal(wk.view(torch.int16), ref[0].view(torch.int16))
         assert torch.equal(wv.view(torch.int16), ref[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("read_bytes,write_bytes,wg", [(32768, 17408, 4), (32768, 0, 8), (4096, 4096, 1)])
+def test_stream_probe_copies_the_written_prefix(read_bytes, write_bytes, wg):
+    """The bench's streaming probe: each 32 KB record's first ``write_bytes``
+    reach dst unchanged; the rest of dst is untouched."""
+    import torch
+
+    from fragpack_amd.ops.fragpack_ext import extension
+
+    n = 37  # fewer records than workgroups, and not a multiple of the grid
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    src = torch.randint(0, 256, (n * 32768,), generator=gen, device="cuda", dtype=torch.uint8)
+    dst = torch.full_like(src, 0xA5)
+    print("probe", read_bytes, write_bytes, wg, flush=True)
+    extension().stream_probe(src, dst, read_bytes, write_bytes, wg)
+    torch.cuda.synchronize()
+    s, d = src.view(n, 32768), dst.view(n, 32768)
+    assert torch.equal(d[:, :write_bytes], s[:, :write_bytes])
+    assert bool((d[:, write_bytes:] == 0xA5).all())
+    with pytest.raises(RuntimeError, match="write <= read"):
+        extension().stream_probe(src, dst, 4096, 8192, wg)
