@@ -57,7 +57,7 @@ def test_from_imports_and_calls():
         assert np.array_equal(decode_record(encode_record(rec, table, kv), table, kv), rec)
     dump = rec.reshape(1, 1, 1, 128, 1, 128).repeat(2, axis=2)
     assert calibrate(dump).shape == (1, 2, 1, 22)
-    assert page_bytes(4) == 190464 and page_bytes(8) == 380928  # SURVEY figures, hbm_kv.py:87-99
+    assert page_bytes(4) == 190464 and page_bytes(8) == 380928  # the reference page sizes, hbm_kv.py:87-99
     assert decode_units(4, 4, 256) >= 4
     o, m, p = workspace_elems(4, 16)
     assert o == 4 * 16 * 8 * 128 and m == 4 * 16 * 8 * 2 and p > 0
