@@ -171,3 +171,24 @@ def test_store_write_rejects_bad_steps_without_gpu_work():
     rc = f(ctypes.byref(d), dummy, 8 * 128, 128, dummy, 8 * 128, 128, dummy, 16, 5, None)
     assert rc == -1 and b"layer" in lib.fp_last_error()
     assert f(ctypes.byref(d), dummy, 8 * 128, 128, dummy, 8 * 128, 128, dummy, 0, 0, None) == 0
+
+
+def test_planner_reciprocal_division_is_exact_within_its_range():
+    """The device planners divide x / d (0 <= x < 2^22, d >= 1) by a float
+    product with the hardware reciprocal (relative error up to one ulp,
+    2^-23) and one correction step each way (fp_attn.hip, ``Divider``).
+    Restated in float32 with the reciprocal taken one ulp low, exact and one
+    ulp high: the quotient equals x // d everywhere sampled, including
+    multiples of d and their neighbours and the range's ends."""
+    rng = np.random.default_rng(7)
+    ds = np.concatenate([np.arange(1, 3000), rng.integers(3000, 1 << 22, 4000), [(1 << 22) - 1]]).astype(np.int64)
+    for d in ds:
+        k = rng.integers(0, ((1 << 22) - 1) // d + 1, 24)
+        x = np.concatenate([k * d, k * d - 1, k * d + d - 1, rng.integers(0, 1 << 22, 24), [0, (1 << 22) - 1]])
+        x = x[(x >= 0) & (x < (1 << 22))]
+        exact = np.float32(1.0) / np.float32(d)
+        for inv in (np.nextafter(exact, np.float32(0)), exact, np.nextafter(exact, np.float32(2))):
+            q = np.trunc(x.astype(np.float32) * np.float32(inv)).astype(np.int64)
+            q += (q + 1) * d <= x
+            q -= q * d > x
+            np.testing.assert_array_equal(q, x // d, err_msg=f"d={d}")
