@@ -766,15 +766,20 @@ attn_kernel(AttnParams pk) {
     // share a CU, dispatched in that order; at equal issue priority the
     // oldest runs ahead (measured at config 4's shape: the three finished
     // their units ~30% apart, the CU idling at the end).  Each page step sets
-    // the priority to (step + age rank) mod 4: at any step the three hold
-    // different priorities, rotating.
+    // the priority to (t + age rank) mod 4, t the device clock
+    // (s_memrealtime, 100 MHz) in 5.12 us quanta: at any moment the three
+    // hold different priorities, rotating in step.  (Rotating by the page
+    // step instead left the oldest a few percent ahead: a workgroup one step
+    // ahead of the next-younger shares its priority and wins the tie by age.
+    // Measured at config 4: 927-933 us against 935-941 by step; 2.56 and
+    // 1.28 us quanta were slower, 10.24 us no faster.)
     const int age = kHalves == 1 ? (int)(blockIdx.y * gridDim.x + blockIdx.x) / max(1, p.slots / kAttnPerCu) : 0;
     // a half takes pages half, half + 2, ...; both halves run the same
     // number of steps (and barriers): a step past a half's pages repeats its
     // last page with every key masked
     const int nsteps = kHalves == 2 ? (npages + 1) >> 1 : npages;
     for (int j = 0; j < nsteps; ++j) {
-      rotate_priority(j + age);
+      rotate_priority(kHalves == 1 ? (int)(__builtin_amdgcn_s_memrealtime() >> 9) + age : j);
       const int i = kHalves == 2 ? min(2 * j + half, npages - 1) : j;  // page of the unit
       const bool act = kHalves == 1 || 2 * j + half < npages;
       const int seq_m = act ? seq : 0;  // context this step's keys are masked against
