@@ -169,6 +169,12 @@ class Extension:
         _check(kvh * group == qsh[1], "query heads must be a multiple of the group")
         if B == 0:
             return
+        # A reusing call reads the unit descriptors an earlier planning call
+        # wrote: without one (same units, batch and heads) they are whatever
+        # the buffer holds, and the kernel would follow them anywhere.
+        _check(replan or getattr(plan, "_fp_plan_key", None) == (units, B, kvh),
+               "replan=False reuses the plan of an earlier call on this workspace with the same units, batch "
+               "and kv heads: plan first")
         # Replanning runs inside the attention kernel (no plan launch) once a
         # call has left this workspace's merge counters at zero; the first
         # call on a workspace launches the planner, which zeroes them.
@@ -194,6 +200,7 @@ class Extension:
                                       "faulted and the cause is not yet found; write with HbmKvStore.write")
         if mode:
             plan._fp_counters_zeroed = True
+            plan._fp_plan_key = (units, B, kvh)
 
     # -- store (fragpack_ext.cpp:11-39, hbm_kv.cu:669-734) --
     def hbm_prepare(self, *args) -> None:

@@ -116,7 +116,8 @@ def decode_attention(
         out: BF16 ``[B, H * G, 128]`` output (rows may be strided).
         workspace: ``(opart, ml, plan)`` sized by :func:`workspace_elems`.
         replan: Recompute the work plan from ``seq_lens`` and ``units``; later
-            layers of the same step may pass False.
+            layers of the same step may pass False (the workspace must then
+            hold a plan made for the same ``units``, batch and KV heads).
         append: None, or ``(new_k, new_v, slot_mapping, staging, scratch)``:
             write each sequence's new token (BF16 ``[B, H, 128]``, int64
             slot, negative = padding; the sequence's last position) into its
@@ -128,6 +129,8 @@ def decode_attention(
 
     Raises:
         ValueError: If the query group does not divide ``GQA``.
+        RuntimeError: If ``replan`` is False and no earlier call planned this
+            workspace for the same units, batch and KV heads.
 
     Async/thread-safety:
         Enqueues on the current stream; not synchronized.  Unlike the

@@ -68,7 +68,10 @@ int fp_abi_version(void);
  *   out         BF16 [B, H * group, 128], out_stride elements between rows
  *   group       query heads per KV head: 1, 2, 4 or 8 (the reference pads
  *               smaller groups to 8 on the host; this kernel takes them as is)
- *   replan      0: reuse the plan in the workspace; 1: plan with a planner
+ *   replan      0: reuse the plan in the workspace (written by an earlier
+ *               planning call with the same units, batch and kv_heads; the
+ *               kernel follows its unit descriptors, so anything else is
+ *               undefined -- the Python mirror refuses such a call); 1: plan with a planner
  *               launch (also zeroes the merge counters); 2: plan inside the
  *               attention kernel when batch <= 64 (else as 1) -- the merge
  *               counters must be zero, as any completed call leaves them;

@@ -192,3 +192,25 @@ def test_planner_reciprocal_division_is_exact_within_its_range():
             q += (q + 1) * d <= x
             q -= q * d > x
             np.testing.assert_array_equal(q, x // d, err_msg=f"d={d}")
+
+
+def test_plan_reuse_without_a_plan_is_refused():
+    """A reusing decode call (replan=False) on a workspace no planning call
+    has written is refused on the host, before any device pointer is taken:
+    the kernel would follow whatever descriptors the buffer holds."""
+    from fragpack_amd.ops.fragpack_ext import extension
+
+    B, H, G, units = 2, 2, 8, 8
+    q = torch.zeros((B, H * G, 128), dtype=torch.bfloat16)
+    out = torch.zeros_like(q)
+    opart, ml, plan = fad.workspace_elems(H, units)
+    ws = (torch.zeros(opart), torch.zeros(ml), torch.zeros(plan, dtype=torch.int32))
+    args = (q, torch.zeros((4, 2, H), dtype=torch.int64), torch.zeros((4, 2, H), dtype=torch.int32),
+            torch.zeros((2, H, 2), dtype=torch.int32), torch.zeros((2, H, 16), dtype=torch.uint8),
+            torch.zeros((B, 4), dtype=torch.int32), torch.ones(B, dtype=torch.int32), *ws, out, units)
+    with pytest.raises(RuntimeError, match="plan first"):
+        extension().fused_decode(*args, False, 0.1, G)
+    # a key from another shape is refused too
+    ws[2]._fp_plan_key = (units + 1, B, H)
+    with pytest.raises(RuntimeError, match="plan first"):
+        extension().fused_decode(*args, False, 0.1, G)
