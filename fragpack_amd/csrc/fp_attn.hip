@@ -779,7 +779,7 @@ attn_kernel(AttnParams pk) {
     // last page with every key masked
     const int nsteps = kHalves == 2 ? (npages + 1) >> 1 : npages;
     for (int j = 0; j < nsteps; ++j) {
-      rotate_priority(kHalves == 1 ? (int)(__builtin_amdgcn_s_memrealtime() >> 9) + age : j);
+      rotate_priority(kHalves == 1 ? (int)(((uint32_t)(__builtin_amdgcn_s_memrealtime() >> 9) + (uint32_t)age) & 3u) : j);
       const int i = kHalves == 2 ? min(2 * j + half, npages - 1) : j;  // page of the unit
       const bool act = kHalves == 1 || 2 * j + half < npages;
       const int seq_m = act ? seq : 0;  // context this step's keys are masked against
